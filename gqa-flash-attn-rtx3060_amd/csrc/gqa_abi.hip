@@ -1,0 +1,154 @@
+// gqa_abi.hip — extern "C" entry points declared in include/gqa_attn.h.
+//
+// Argument validation mirrors the asserts of reference
+// gqa_kernels/dispatch.py:30-33 (divisible heads, head_dim in {64, 128}) plus
+// the layout requirements of the vectorised kernels (unit last-dim stride,
+// 16-byte aligned rows).  Nothing here allocates device memory.
+#include <hip/hip_runtime.h>
+
+#include "../../include/gqa_attn.h"
+#include "gqa_params.hpp"
+
+namespace {
+
+using gqa::Dims;
+using gqa::TensorRef;
+
+constexpr int kAbiVersion = 1;
+
+int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
+  if (Hq % Hkv != 0) return GQA_E_SHAPE;
+  if (D != 64 && D != 128) return GQA_E_HEAD_DIM;
+  if (dtype != GQA_DTYPE_BF16 && dtype != GQA_DTYPE_FP16) return GQA_E_DTYPE;
+  return GQA_OK;
+}
+
+// Rows must start on 16 bytes: pointer and the three outer strides (in
+// 2-byte elements) multiples of 8; the last-dim stride must be 1.
+int check_tensor(const void* ptr, const int64_t st[4]) {
+  if (ptr == nullptr || st == nullptr) return GQA_E_NULL;
+  if (st[3] != 1) return GQA_E_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return GQA_E_STRIDE;
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % 8 != 0) return GQA_E_STRIDE;
+  return GQA_OK;
+}
+
+TensorRef ref(const void* ptr, const int64_t st[4]) { return TensorRef{ptr, st[0], st[1], st[2]}; }
+
+int to_code(hipError_t e) { return e == hipSuccess ? GQA_OK : static_cast<int>(e); }
+
+}  // namespace
+
+extern "C" {
+
+int gqa_abi_version(void) { return kAbiVersion; }
+
+const char* gqa_strerror(int code) {
+  switch (code) {
+    case GQA_OK: return "success";
+    case GQA_E_SHAPE: return "invalid shape: sizes must be non-negative and num_heads divisible by num_kv_heads";
+    case GQA_E_HEAD_DIM: return "unsupported head_dim (supported: 64, 128)";
+    case GQA_E_DTYPE: return "unsupported dtype (supported: bf16, fp16)";
+    case GQA_E_STRIDE: return "unsupported layout: last dim must be contiguous and rows 16-byte aligned";
+    case GQA_E_SPLITS: return "splits out of range [1, GQA_MAX_SPLITS]";
+    case GQA_E_GROUP: return "group size (num_heads / num_kv_heads) larger than 128";
+    case GQA_E_NULL: return "null pointer argument";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown error";
+}
+
+int gqa_device_cu_count(int device) {
+  int n = 0;
+  hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  return n;
+}
+
+size_t gqa_split_workspace_bytes(int batch, int num_heads, int seq_q, int head_dim, int splits) {
+  if (batch <= 0 || num_heads <= 0 || seq_q <= 0 || head_dim <= 0 || splits <= 0) return 0;
+  const size_t rows = (size_t)batch * num_heads * seq_q * splits;
+  return rows * ((size_t)head_dim + 2) * sizeof(float);
+}
+
+int gqa_fwd_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                   const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], int batch,
+                   int num_heads, int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2,
+                   int causal, int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
+  if (rc) return rc;
+  const int G = num_heads / num_kv_heads;
+  if (G > gqa::kFwdRows) return GQA_E_GROUP;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
+  if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
+
+  gqa::FwdParams p;
+  p.q = ref(q, q_stride);
+  p.k = ref(k, k_stride);
+  p.v = ref(v, v_stride);
+  p.o = ref(o, o_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, G, scale_log2, causal ? 1 : 0};
+  p.block_m = gqa::kFwdRows / G;
+  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  return to_code(gqa::launch_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                           const void* v, const int64_t v_stride[4], float* workspace, int splits, int batch,
+                           int num_heads, int num_kv_heads, int seq_q, int seq_kv, int head_dim,
+                           float scale_log2, int causal, int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
+  if (rc) return rc;
+  if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (workspace == nullptr) return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return GQA_E_STRIDE;
+  if ((rc = check_tensor(q, q_stride))) return rc;
+  if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
+
+  const int G = num_heads / num_kv_heads;
+  gqa::SplitParams p;
+  p.q = ref(q, q_stride);
+  p.k = ref(k, k_stride);
+  p.v = ref(v, v_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, G, scale_log2, causal ? 1 : 0};
+  const size_t rows = (size_t)batch * num_heads * seq_q * splits;
+  p.ws_acc = workspace;
+  p.ws_m = workspace + rows * head_dim;
+  p.ws_l = p.ws_m + rows;
+  p.splits = splits;
+  p.chunk = (seq_kv + splits - 1) / splits;
+  p.n_rblk = (G * seq_q + 31) / 32;
+  return to_code(gqa::launch_split_first(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gqa_split_reduce_launch(const float* workspace, int splits, void* o, const int64_t o_stride[4], int batch,
+                            int num_heads, int seq_q, int head_dim, int dtype, void* stream) {
+  if (batch < 0 || num_heads <= 0 || seq_q < 0) return GQA_E_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return GQA_E_HEAD_DIM;
+  if (dtype != GQA_DTYPE_BF16 && dtype != GQA_DTYPE_FP16) return GQA_E_DTYPE;
+  if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (workspace == nullptr) return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return GQA_E_STRIDE;
+  int rc = check_tensor(o, o_stride);
+  if (rc) return rc;
+  gqa::ReduceParams p;
+  const size_t rows = (size_t)batch * num_heads * seq_q * splits;
+  p.ws_acc = workspace;
+  p.ws_m = workspace + rows * head_dim;
+  p.ws_l = p.ws_m + rows;
+  p.o = ref(o, o_stride);
+  p.B = batch;
+  p.Hq = num_heads;
+  p.Sq = seq_q;
+  p.D = head_dim;
+  p.splits = splits;
+  return to_code(gqa::launch_split_reduce(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// gqa_params.hpp — kernel parameter blocks and the launchers each kernel
+// translation unit exports to the C-ABI layer (gqa_abi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gqa {
+
+// Strides are in elements; the head_dim stride is 1 (checked by the ABI).
+struct TensorRef {
+  const void* ptr;
+  int64_t sb, sh, ss;  // batch, head, sequence strides
+};
+
+struct Dims {
+  int B, Hq, Hkv, Sq, Skv, D, G;
+  float c;  // head_dim^-0.5 * log2(e)
+  int causal;
+};
+
+// Single-pass group-packed forward.
+struct FwdParams {
+  TensorRef q, k, v, o;
+  Dims dm;
+  int block_m;  // query positions per workgroup (G * block_m <= 128 packed rows)
+  int n_mblk;   // ceil(Sq / block_m)
+};
+
+// Split-KV first pass: one workgroup per (b, kv head, row block, split).
+struct SplitParams {
+  TensorRef q, k, v;
+  Dims dm;
+  float* ws_acc;  // (B, Hq, Sq, splits, D)
+  float* ws_m;    // (B, Hq, Sq, splits), log2 units
+  float* ws_l;    // (B, Hq, Sq, splits)
+  int splits;
+  int chunk;   // ceil(Skv / splits)
+  int n_rblk;  // ceil(G * Sq / 32)
+};
+
+// Split-KV combine: one workgroup per (b, q head, query row).
+struct ReduceParams {
+  const float* ws_acc;
+  const float* ws_m;
+  const float* ws_l;
+  TensorRef o;
+  int B, Hq, Sq, D, splits;
+};
+
+// Packed query rows per single-pass workgroup (4 waves x 32 rows).
+constexpr int kFwdRows = 128;
+// Keys per single-pass LDS tile, and per split-KV LDS tile.
+constexpr int kFwdTileKeys = 64;
+constexpr int kSplitTileKeys = 128;
+
+hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream);
+hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream);
+hipError_t launch_split_reduce(const ReduceParams& p, int dtype, hipStream_t stream);
+
+}  // namespace gqa

@@ -1,0 +1,282 @@
+// gqa_split.hip — split-KV decode path for gfx950: first pass + LSE combine.
+//
+// Replaces the Triton kernels gqa_split_first_kernel and
+// gqa_split_reduce_kernel (reference gqa_kernels/gqa_split.py:26-147).
+//
+// First pass: one workgroup per (batch, kv head, 32-row block, split).  The
+// packed rows are the G*Sq (head, position) pairs of one kv head, position
+// major (row r -> position r / G, head r % G), so a decode step (Sq = 1) packs
+// its whole query group into one MFMA N block and the K/V of the chunk is read
+// from HBM exactly once.  The chunk is streamed in 128-key tiles through LDS
+// (the next tile's loads are in flight during compute); each of the 4 waves
+// runs its own online softmax over 32 keys of every tile, and the 4 partial
+// states are merged in LDS before one fp32 partial (m, l, unnormalised acc)
+// per row is written (gqa_split.py:102-112).  Chunk bounds follow
+// gqa_split.py:55-60, including the causal clamp to the block's last visible
+// key; a chunk with no visible key stores m = -inf, l = 0, acc = 0.
+//
+// Combine: one workgroup per (batch, q head, row):
+//   m* = max m_s, a_s = exp2(m_s - m*), l* = sum a_s l_s,
+//   o = sum a_s acc_s / l*                         (gqa_split.py:134-147)
+#include "gqa_common.hpp"
+#include "gqa_params.hpp"
+
+namespace gqa {
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void gqa_split_first_kernel(SplitParams p) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  using ST = SubTile<D>;
+  // One 128-key tile = two 64-key sub-tiles; reused for the final merge.
+  __shared__ __attribute__((aligned(16))) char smem[2 * ST::kBytes];
+  __shared__ float m_s[128], l_s[128];
+
+  const Dims& dm = p.dm;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int i = lane & 31, hh = lane >> 5;
+
+  const int total = dm.B * dm.Hkv * p.n_rblk * p.splits;
+  const int w = xcd_remap(blockIdx.x, total);
+  const int s = w % p.splits;
+  int rest = w / p.splits;
+  const int rb = rest % p.n_rblk;
+  rest /= p.n_rblk;
+  const int kvh = rest % dm.Hkv;
+  const int b = rest / dm.Hkv;
+
+  // This lane's query row (position-major packing).
+  const int r = 32 * rb + i;
+  const int pos = r / dm.G, g = r - pos * dm.G;
+  const bool valid = pos < dm.Sq;
+  const int head = kvh * dm.G + g;
+  const int qpos = pos + (dm.Skv - dm.Sq);
+
+  u32x4 qreg[D / 16];
+  {
+    const T* qrow = static_cast<const T*>(p.q.ptr) + (int64_t)b * p.q.sb + (int64_t)head * p.q.sh +
+                    (int64_t)(valid ? pos : 0) * p.q.ss;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (valid) x = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
+      qreg[ks] = x;
+    }
+  }
+
+  // Keys of this chunk, clamped to the block's last visible key.
+  const int c0 = s * p.chunk;
+  int c1 = min(c0 + p.chunk, dm.Skv);
+  const int pos_lo = (32 * rb) / dm.G;
+  const int pos_hi = min(dm.Sq - 1, (32 * rb + 31) / dm.G);
+  if (dm.causal) c1 = min(c1, pos_hi + (dm.Skv - dm.Sq) + 1);
+  const int ntiles = c1 > c0 ? (c1 - c0 + kSplitTileKeys - 1) / kSplitTileKeys : 0;
+  const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
+
+  const T* kbase = static_cast<const T*>(p.k.ptr) + (int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh;
+  const T* vbase = static_cast<const T*>(p.v.ptr) + (int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh;
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) acc[db] = f32x16{};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+  const float c = dm.c;
+
+  SubTileRegs<D> R0, R1;
+  if (ntiles > 0) {
+    load_subtile<D, T>(R0, kbase, vbase, p.k.ss, p.v.ss, c0, c1, t);
+    load_subtile<D, T>(R1, kbase, vbase, p.k.ss, p.v.ss, c0 + 64, c1, t);
+  }
+  const int sub = wave >> 1, mb = wave & 1;
+  const char* mytile = smem + sub * ST::kBytes;
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int key0 = c0 + it * kSplitTileKeys;
+    __syncthreads();  // previous tile fully consumed
+    store_subtile<D>(smem, R0, t);
+    store_subtile<D>(smem + ST::kBytes, R1, t);
+    __syncthreads();
+    if (it + 1 < ntiles) {
+      load_subtile<D, T>(R0, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys, c1, t);
+      load_subtile<D, T>(R1, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys + 64, c1, t);
+    }
+
+    const int kb0 = key0 + 32 * wave;  // this wave's 32 keys
+    if (kb0 >= c1) continue;           // wave-uniform: nothing visible here
+    f32x16 sc = qk_block<DT, D>(mytile, qreg, mb, lane);
+    const bool need_mask = (kb0 + 32 > c1) || (dm.causal && kb0 + 31 > qpos_lo);
+    if (need_mask) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = kb0 + key_of(v, hh);
+        if (key >= c1 || (dm.causal && key > qpos)) sc[v] = -__builtin_inff();
+      }
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[v]);
+    mx = xhalf_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = fast_exp2((m_run - m_use) * c);
+    const float nmc = -m_use * c;
+    float pv[16];
+    float rs = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      pv[v] = fast_exp2(__builtin_fmaf(sc[v], c, nmc));
+      rs += pv[v];
+    }
+    u32x4 pk[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pk[kk][e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
+    pv_block<DT, D>(mytile, pk, acc, mb, lane);
+  }
+
+  // Merge the 4 waves' states in LDS: m_s/l_s [wave][row], acc (reusing the
+  // tile buffer, exactly 4 * D * 32 floats) as f32x4 at
+  // [((wave * D/32 + db) * 4 + j) * 64 + lane].
+  static_assert(4 * D * 32 * sizeof(float) <= 2 * ST::kBytes, "merge buffer");
+  const float l_tot = xhalf_sum(l_run);
+  __syncthreads();
+  f32x4* a_s = reinterpret_cast<f32x4*>(smem);
+  if (hh == 0) {
+    m_s[wave * 32 + i] = m_run;
+    l_s[wave * 32 + i] = l_tot;
+  }
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f32x4 x = {acc[db][4 * j], acc[db][4 * j + 1], acc[db][4 * j + 2], acc[db][4 * j + 3]};
+      a_s[((wave * (D / 32) + db) * 4 + j) * 64 + lane] = x;
+    }
+  __syncthreads();
+  if (wave < D / 32) {
+    const int db = wave;
+    float mw[4];
+    float mstar = -__builtin_inff();
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      mw[ww] = m_s[ww * 32 + i];
+      mstar = fmaxf(mstar, mw[ww]);
+    }
+    const float mstar_use = (mstar == -__builtin_inff()) ? 0.f : mstar;
+    float lsum = 0.f;
+    f32x4 o[4] = {};
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float f = fast_exp2((mw[ww] - mstar_use) * c);
+      lsum += f * l_s[ww * 32 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] += f * a_s[((ww * (D / 32) + db) * 4 + j) * 64 + lane];
+    }
+    if (valid) {
+      const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
+      float* wa = p.ws_acc + row * D;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(wa + 32 * db + 8 * j + 4 * hh) = o[j];
+      if (db == 0 && hh == 0) {
+        p.ws_m[row] = mstar * c;
+        p.ws_l[row] = lsum;
+      }
+    }
+  }
+}
+
+// LSE combine.  256 threads: thread (d4, sg) owns output columns
+// [4*d4, 4*d4 + 4) and the splits sg, sg + NSG, ...
+template <int DT, int D>
+__global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  constexpr int ND4 = D / 4;
+  constexpr int NSG = 256 / ND4;
+  __shared__ float red_m[256];
+  __shared__ f32x4 red_o[NSG][ND4];
+  __shared__ float red_l[NSG][ND4];
+
+  const int t = threadIdx.x;
+  const int row = blockIdx.x;  // ((b * Hq + h) * Sq + pos)
+  const int S = p.splits;
+  const float* wm = p.ws_m + (int64_t)row * S;
+  const float* wl = p.ws_l + (int64_t)row * S;
+  const float* wa = p.ws_acc + (int64_t)row * S * D;
+
+  float mx = -__builtin_inff();
+  for (int s = t; s < S; s += 256) mx = fmaxf(mx, wm[s]);
+  red_m[t] = mx;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) red_m[t] = fmaxf(red_m[t], red_m[t + off]);
+    __syncthreads();
+  }
+  const float mstar = red_m[0];
+
+  const int d4 = t % ND4, sg = t / ND4;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+  for (int s = sg; s < S; s += NSG) {
+    // exp2(-inf - -inf) = NaN when every chunk is empty, as gqa_split.py:138.
+    const float a = fast_exp2(wm[s] - mstar);
+    l += a * wl[s];
+    o += a * *reinterpret_cast<const f32x4*>(wa + (int64_t)s * D + 4 * d4);
+  }
+  red_o[sg][d4] = o;
+  red_l[sg][d4] = l;
+  __syncthreads();
+  if (sg == 0) {
+    for (int k = 1; k < NSG; ++k) {
+      o += red_o[k][d4];
+      l += red_l[k][d4];
+    }
+    const int pos = row % p.Sq;
+    const int bh = row / p.Sq;
+    const int h = bh % p.Hq, b = bh / p.Hq;
+    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh +
+              (int64_t)pos * p.o.ss;
+    u32x2 x;
+    x[0] = E::pack2(o[0] / l, o[1] / l);
+    x[1] = E::pack2(o[2] / l, o[3] / l);
+    *reinterpret_cast<u32x2*>(orow + 4 * d4) = x;
+  }
+}
+
+template <int DT, int D>
+static hipError_t launch_split_first_t(const SplitParams& p, hipStream_t stream) {
+  const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * p.n_rblk * p.splits;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL((gqa_split_first_kernel<DT, D>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int DT, int D>
+static hipError_t launch_split_reduce_t(const ReduceParams& p, hipStream_t stream) {
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL((gqa_split_reduce_kernel<DT, D>), dim3((unsigned)rows), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream) {
+  if (dtype == 0)
+    return p.dm.D == 128 ? launch_split_first_t<0, 128>(p, stream) : launch_split_first_t<0, 64>(p, stream);
+  return p.dm.D == 128 ? launch_split_first_t<1, 128>(p, stream) : launch_split_first_t<1, 64>(p, stream);
+}
+
+hipError_t launch_split_reduce(const ReduceParams& p, int dtype, hipStream_t stream) {
+  if (dtype == 0)
+    return p.D == 128 ? launch_split_reduce_t<0, 128>(p, stream) : launch_split_reduce_t<0, 64>(p, stream);
+  return p.D == 128 ? launch_split_reduce_t<1, 128>(p, stream) : launch_split_reduce_t<1, 64>(p, stream);
+}
+
+}  // namespace gqa

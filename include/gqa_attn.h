@@ -1,0 +1,105 @@
+/*
+ * gqa_attn.h — C ABI of the MI355X (gfx950) GQA flash-attention forward.
+ *
+ * Every entry point takes plain device pointers, int64 element strides and
+ * int sizes, enqueues its kernels on the given HIP stream and returns at once
+ * (asynchronous, like the Triton launches it replaces).  The library never
+ * allocates device memory: outputs and the split-KV workspace are owned by the
+ * caller.  Return value: 0 on success, a GQA_E* code below for rejected
+ * arguments, or a hipError_t value (>0) reported by the launch.
+ *
+ * Layouts (element strides, index order b, h, s, d), as in the reference
+ * gqa_kernels/dispatch.py:17-27:
+ *   q : (batch, num_heads,    seq_q,  head_dim)
+ *   k : (batch, num_kv_heads, seq_kv, head_dim)
+ *   v : (batch, num_kv_heads, seq_kv, head_dim)
+ *   o : (batch, num_heads,    seq_q,  head_dim)
+ * The last dimension must be contiguous (stride 1) and each row 16-byte
+ * aligned (reference README.md:112 states last-dim contiguity as an invariant).
+ *
+ * Semantics (reference tests/reference.py:16-34): q head h reads kv head
+ * h / (num_heads / num_kv_heads); scores are scaled by head_dim^-0.5 (passed
+ * here as scale_log2 = head_dim^-0.5 * log2(e), dispatch.py:48); with causal,
+ * query row i attends keys [0, i + seq_kv - seq_q] (bottom-right alignment).
+ */
+#ifndef GQA_ATTN_H
+#define GQA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes for q, k, v and o (all four share one dtype). */
+#define GQA_DTYPE_BF16 0
+#define GQA_DTYPE_FP16 1
+
+/* Error codes (negative, to stay clear of hipError_t values). */
+#define GQA_OK 0
+#define GQA_E_SHAPE (-1)      /* non-positive size or num_heads % num_kv_heads != 0 */
+#define GQA_E_HEAD_DIM (-2)   /* head_dim not in {64, 128} (dispatch.py:32) */
+#define GQA_E_DTYPE (-3)      /* dtype code not GQA_DTYPE_BF16 / GQA_DTYPE_FP16 */
+#define GQA_E_STRIDE (-4)     /* last-dim stride != 1 or rows not 16-byte aligned */
+#define GQA_E_SPLITS (-5)     /* splits outside [1, GQA_MAX_SPLITS] */
+#define GQA_E_GROUP (-6)      /* group size above what one packed tile holds */
+#define GQA_E_NULL (-7)       /* null pointer argument */
+
+#define GQA_MAX_SPLITS 1024
+
+/* ABI revision; bumped when a signature below changes. */
+int gqa_abi_version(void);
+
+/* Message for a return code (GQA_E* or hipError_t).  Never NULL. */
+const char* gqa_strerror(int code);
+
+/* Number of compute units of HIP device `device` (256 on MI355X), or a
+ * negative value on error.  Replaces the hard-coded SM_COUNT = 28 of
+ * reference gqa_kernels/dispatch.py:10. */
+int gqa_device_cu_count(int device);
+
+/* Single-pass group-packed forward: o = softmax(q k^T * scale) v.
+ * Replaces the launch of gqa_fwd_kernel at reference
+ * gqa_kernels/dispatch.py:49-61 (kernel gqa_kernels/gqa_fwd.py:33-109). */
+int gqa_fwd_launch(const void* q, const int64_t q_stride[4],
+                   const void* k, const int64_t k_stride[4],
+                   const void* v, const int64_t v_stride[4],
+                   void* o, const int64_t o_stride[4],
+                   int batch, int num_heads, int num_kv_heads,
+                   int seq_q, int seq_kv, int head_dim,
+                   float scale_log2, int causal, int dtype, void* stream);
+
+/* Bytes of fp32 workspace the split-KV path needs for `splits` chunks:
+ * acc (batch, num_heads, seq_q, splits, head_dim) followed by m and l
+ * (batch, num_heads, seq_q, splits) each — the partial tensors of reference
+ * gqa_kernels/gqa_split.py:160-163, packed into one buffer. */
+size_t gqa_split_workspace_bytes(int batch, int num_heads, int seq_q,
+                                 int head_dim, int splits);
+
+/* Split-KV first pass: per-chunk partial (m, l, unnormalised acc) in fp32,
+ * m and l in log2 units.  Replaces reference gqa_kernels/gqa_split.py:168-183
+ * (kernel gqa_split.py:26-112).  Chunk s covers keys
+ * [s*ceil(seq_kv/splits), (s+1)*ceil(seq_kv/splits)) ∩ [0, seq_kv). */
+int gqa_split_first_launch(const void* q, const int64_t q_stride[4],
+                           const void* k, const int64_t k_stride[4],
+                           const void* v, const int64_t v_stride[4],
+                           float* workspace, int splits,
+                           int batch, int num_heads, int num_kv_heads,
+                           int seq_q, int seq_kv, int head_dim,
+                           float scale_log2, int causal, int dtype,
+                           void* stream);
+
+/* Split-KV second pass: log-sum-exp combine of the partials into o.
+ * Replaces reference gqa_kernels/gqa_split.py:185-193
+ * (kernel gqa_split.py:115-147). */
+int gqa_split_reduce_launch(const float* workspace, int splits,
+                            void* o, const int64_t o_stride[4],
+                            int batch, int num_heads, int seq_q, int head_dim,
+                            int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GQA_ATTN_H */

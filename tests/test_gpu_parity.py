@@ -1,0 +1,282 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Cases mirror reference tests/test_correctness.py:48-77 (x0.1 inputs at the
+reference's tolerances) and the BASELINE configs (N(0,1) inputs, max abs
+<= 2e-2 / mean abs <= 2e-3 for bf16), plus edge cases the reference leaves
+implicit: ragged lengths, other group sizes and head_dim 64, non-causal,
+strided inputs, fully masked rows and split-count invariance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (BASELINE_TOL, REF_TOL, assert_close, errors, make_inputs, oracle, to_np,
+                     torch_reference_gpu)
+from oracle.gqa_oracle import split_partials
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+def _attn():
+    from gqa_kernels import gqa_flash_attn
+    return gqa_flash_attn
+
+
+def _route(q, k):
+    from gqa_kernels.dispatch import _cu_count, choose_route
+    B, Hq, Sq, _ = q.shape
+    return choose_route(B, Hq, k.shape[1], Sq, k.shape[2], _cu_count(0))
+
+
+def _run(q, k, v, causal=True):
+    out = _attn()(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    return out
+
+
+# --------------------------------------------------------------------------
+# The reference's own cases (Llama-3.1-8B shape, x0.1 inputs, seed 0).
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seq_len", [512, 2048, 4096])
+def test_prefill(seq_len, dtype):
+    q, k, v = make_inputs(1, 32, 8, seq_len, seq_len, 128, dtype, scale=0.1, device=DEV)
+    out = _run(q, k, v)
+    assert out.shape == q.shape and out.dtype == dtype
+    assert_close(out, oracle(q, k, v), REF_TOL[dtype], f"prefill {seq_len}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seq_kv", [512, 2048, 4096, 8192])
+def test_decode(seq_kv, dtype):
+    q, k, v = make_inputs(1, 32, 8, 1, seq_kv, 128, dtype, scale=0.1, device=DEV)
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v), REF_TOL[dtype], f"decode {seq_kv}")
+
+
+@pytest.mark.parametrize("seq_q,seq_kv", [(16, 1024), (64, 2048), (256, 4096)])
+def test_chunked_prefill(seq_q, seq_kv):
+    q, k, v = make_inputs(1, 32, 8, seq_q, seq_kv, 128, torch.bfloat16, scale=0.1, device=DEV)
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v), REF_TOL[torch.bfloat16], f"chunked {seq_q}/{seq_kv}")
+
+
+# --------------------------------------------------------------------------
+# BASELINE configs, N(0,1) inputs.
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("seq", [2048, 4096])
+def test_baseline_prefill_full(seq):
+    q, k, v = make_inputs(1, 32, 8, seq, seq, 128, device=DEV)
+    assert _route(q, k).kind == "single"
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], f"prefill {seq}")
+
+
+@pytest.mark.parametrize("seq", [8192, 16384])
+def test_baseline_prefill_large(seq):
+    q, k, v = make_inputs(1, 32, 8, seq, seq, 128, device=DEV)
+    out = _run(q, k, v)
+    # Oracle on row slices at the start, middle and end of every head ...
+    rows = np.r_[0:96, seq // 2 - 48:seq // 2 + 48, seq - 96:seq]
+    assert_close(out[:, :, rows], oracle(q, k, v, rows=rows), BASELINE_TOL[torch.bfloat16],
+                 f"prefill {seq} oracle rows")
+    # ... and a plain fp32 torch reference over every row.
+    ref = torch_reference_gpu(q, k, v)
+    mx, mn = errors(out, ref)
+    assert mx <= 2e-2 and mn <= 2e-3, (mx, mn)
+
+
+@pytest.mark.parametrize("seq_kv", [8192, 32768, 131072])
+def test_baseline_decode(seq_kv):
+    q, k, v = make_inputs(1, 32, 8, 1, seq_kv, 128, device=DEV)
+    assert _route(q, k).kind == "split"
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], f"decode {seq_kv}")
+
+
+def test_baseline_chunked_prefill():
+    q, k, v = make_inputs(4, 32, 8, 512, 8192, 128, device=DEV)
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], "chunked B=4 512/8192")
+
+
+def test_baseline_70b_shape():
+    B, Hq, Hkv, Sq, Skv, D = 16, 64, 8, 4, 32768, 128
+    g = torch.Generator(device=DEV).manual_seed(0)
+    q = torch.randn(B, Hq, Sq, D, device=DEV, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, Skv, D, device=DEV, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, Skv, D, device=DEV, generator=g).to(torch.bfloat16)
+    r = _route(q, k)
+    assert r.kind == "split" and r.workgroups >= 1024, r
+    out = _run(q, k, v)
+    for b in (0, 7, 15):  # oracle on a deterministic subset of batch entries
+        sl = slice(b, b + 1)
+        assert_close(out[sl], oracle(q[sl], k[sl], v[sl]), BASELINE_TOL[torch.bfloat16], f"70B b={b}")
+
+
+# --------------------------------------------------------------------------
+# Closed forms and invariants on the GPU path.
+# --------------------------------------------------------------------------
+def test_prefill_row0_is_first_value_row():
+    # Causal prefill row 0 sees exactly key 0 with p = 1: o = v[kv head, 0]
+    # bit for bit (single visible key, P = 1 exactly, l = 1).
+    q, k, v = make_inputs(1, 32, 8, 300, 300, 128, device=DEV)
+    out = _run(q, k, v)
+    exp = v[:, torch.arange(32, device=DEV) // 4, 0]
+    assert torch.equal(out[:, :, 0], exp)
+
+
+def test_constant_value_rows():
+    q, k, v = make_inputs(2, 8, 2, 70, 333, 128, device=DEV)
+    v = torch.full_like(v, 1.5)
+    for causal in (True, False):
+        out = _run(q, k, v, causal)
+        assert torch.all(out == 1.5)
+
+
+def test_head_map():
+    # V of kv head j is the constant j: output of q head h must be h // G.
+    q, k, v = make_inputs(1, 32, 8, 40, 2048, 128, device=DEV)
+    v = torch.arange(8, device=DEV, dtype=torch.bfloat16).view(1, 8, 1, 1).expand_as(v).contiguous()
+    for (sq, skv) in ((40, 2048), (1, 2048)):
+        out = _run(q[:, :, :sq], k[:, :, :skv], v[:, :, :skv])
+        exp = (torch.arange(32, device=DEV) // 4).to(out.dtype).view(1, 32, 1, 1).expand_as(out)
+        assert torch.equal(out, exp)
+
+
+def test_chunked_equals_prefill_tail():
+    q, k, v = make_inputs(1, 16, 4, 1024, 1024, 128, device=DEV)
+    full = _run(q, k, v)
+    for sq in (1, 7, 64, 300):
+        part = _run(q[:, :, -sq:].contiguous(), k, v)
+        mx, mn = errors(part, to_np(full[:, :, -sq:]))
+        assert mx <= 1.6e-2 and mn <= 1e-3, (sq, mx, mn)
+
+
+def test_decode_causal_equals_noncausal():
+    q, k, v = make_inputs(2, 32, 8, 1, 5000, 128, device=DEV)
+    a = _run(q, k, v, True)
+    b = _run(q, k, v, False)
+    assert torch.equal(a, b)
+
+
+def test_deterministic():
+    q, k, v = make_inputs(1, 32, 8, 777, 777, 128, device=DEV)
+    assert torch.equal(_run(q, k, v), _run(q, k, v))
+    q, k, v = make_inputs(1, 32, 8, 1, 9000, 128, device=DEV)
+    assert torch.equal(_run(q, k, v), _run(q, k, v))
+
+
+# --------------------------------------------------------------------------
+# Split-KV path: partials and split-count invariance.
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("sq,skv,causal", [(1, 3000, True), (5, 2600, True), (16, 1024, True),
+                                           (3, 4100, False), (40, 200, True)])
+def test_split_partials_match_oracle(sq, skv, causal):
+    from gqa_kernels import _lib
+    from gqa_kernels.gqa_split import LOG2E, workspace_bytes
+    B, Hq, Hkv, D, S = 2, 16, 4, 128, 8
+    q, k, v = make_inputs(B, Hq, Hkv, sq, skv, D, device=DEV)
+    lib = _lib.load()
+    ws = torch.empty(workspace_bytes(B, Hq, sq, D, S) // 4, dtype=torch.float32, device=DEV)
+    _lib.check(lib.gqa_split_first_launch(
+        q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k), v.data_ptr(), _lib.strides(v),
+        ws.data_ptr(), S, B, Hq, Hkv, sq, skv, D, D ** -0.5 * LOG2E, int(causal), _lib.DTYPE_BF16,
+        torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    rows = B * Hq * sq * S
+    acc = ws[:rows * D].view(B, Hq, sq, S, D).cpu().numpy()
+    m = ws[rows * D:rows * D + rows].view(B, Hq, sq, S).cpu().numpy()
+    l = ws[rows * D + rows:rows * (D + 2)].view(B, Hq, sq, S).cpu().numpy()
+    m_o, l_o, acc_o = split_partials(to_np(q), to_np(k), to_np(v), causal, S)
+    empty = np.isneginf(m_o)
+    assert np.array_equal(np.isneginf(m), empty)
+    assert np.all(l[empty] == 0) and np.all(acc[empty] == 0)
+    full = ~empty
+    assert np.abs(m[full] - m_o[full]).max() < 1e-3
+    assert np.abs(l[full] / l_o[full] - 1).max() < 1e-4
+    norm = acc[full] / l[full][:, None]
+    norm_o = acc_o[full] / l_o[full][:, None]
+    assert np.abs(norm - norm_o).max() < 1e-2
+
+
+def test_split_count_invariance():
+    from gqa_kernels.gqa_split import split_kv_forward
+    for (sq, skv) in ((1, 4096), (4, 3001), (16, 2048)):
+        q, k, v = make_inputs(1, 32, 8, sq, skv, 128, device=DEV)
+        ref = oracle(q, k, v)
+        for S in (1, 2, 3, 16, 64, 256):
+            out = split_kv_forward(q, k, v, True, S)
+            torch.cuda.synchronize()
+            assert_close(out, ref, BASELINE_TOL[torch.bfloat16], f"split {S} sq={sq} skv={skv}")
+
+
+# --------------------------------------------------------------------------
+# Shapes and layouts beyond the Llama-8B shape.
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D", [
+    (2, 8, 8, 100, 100, 128),     # MHA (G = 1), ragged tiles
+    (1, 16, 2, 33, 257, 64),      # G = 8, head_dim 64, chunked
+    (3, 12, 4, 129, 129, 128),    # G = 3 (block of 42 positions)
+    (1, 32, 1, 65, 2000, 128),    # MQA G = 32
+    (2, 8, 4, 1, 1100, 64),       # decode, head_dim 64, split path
+    (1, 64, 8, 4, 3000, 128),     # 70B group, split path
+    (1, 8, 2, 1, 77, 128),        # short decode, single-pass path
+])
+@pytest.mark.parametrize("causal", [True, False])
+def test_shapes(B, Hq, Hkv, Sq, Skv, D, causal):
+    q, k, v = make_inputs(B, Hq, Hkv, Sq, Skv, D, device=DEV, seed=3)
+    out = _run(q, k, v, causal)
+    assert_close(out, oracle(q, k, v, causal), BASELINE_TOL[torch.bfloat16], "shape")
+
+
+@pytest.mark.parametrize("sq,skv", [(2048, 2048), (1, 8192), (300, 1200)])
+def test_fp16_unit_normal(sq, skv):
+    q, k, v = make_inputs(1, 32, 8, sq, skv, 128, torch.float16, device=DEV)
+    out = _run(q, k, v)
+    assert out.dtype == torch.float16
+    assert_close(out, oracle(q, k, v), BASELINE_TOL[torch.float16], "fp16")
+
+
+def test_strided_inputs():
+    # q from a (B, S, H, D) buffer, K/V as a prefix view of a longer cache.
+    B, Hq, Hkv, Sq, Skv, D = 2, 32, 8, 200, 1500, 128
+    g = torch.Generator(device="cpu").manual_seed(5)
+    qb = torch.randn(B, Sq, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    kc = torch.randn(B, Hkv, Skv + 512, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, Hkv, Skv + 512, D, generator=g).to(torch.bfloat16).to(DEV)
+    q = qb.transpose(1, 2)
+    k, v = kc[:, :, :Skv], vc[:, :, :Skv]
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], "strided")
+    # decode against the strided cache (split path)
+    out1 = _run(q[:, :, -1:], k, v)
+    assert_close(out1, oracle(q[:, :, -1:], k, v), BASELINE_TOL[torch.bfloat16], "strided decode")
+
+
+def test_fully_masked_rows_are_nan():
+    # seq_q > seq_kv under causal: rows with q_pos < 0 see no key; the
+    # reference (kernel and oracle) produce NaN there.
+    q, k, v = make_inputs(1, 8, 2, 40, 24, 128, device=DEV)
+    out = _run(q, k, v)
+    ref = oracle(q, k, v)
+    nan_rows = np.isnan(ref).all(axis=-1)
+    assert nan_rows[:, :, :16].all() and not nan_rows[:, :, 16:].any()
+    assert torch.isnan(out[:, :, :16]).all()
+    assert_close(out[:, :, 16:], ref[:, :, 16:], BASELINE_TOL[torch.bfloat16], "masked")
+
+
+def test_empty_query():
+    q, k, v = make_inputs(1, 8, 2, 0, 64, 128, device=DEV)
+    out = _run(q, k, v)
+    assert out.shape == (1, 8, 0, 128)
