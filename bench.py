@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GQA flash-attention forward (gqa_flash_attn).
+
+Prints ONE JSON line (rank 0).  The headline ``value`` is causal-prefill
+TFLOP/s at the Llama-3.1-8B GQA shape, seq 16384 (B=1, Hq=32, Hkv=8, D=128,
+bf16); the ``decode`` object carries split-KV decode at seq_kv 131072
+(microseconds and HBM GB/s).  Timing follows reference benchmark/run.py:140-154
+(untimed warm-up calls, then back-to-back calls of the full public function
+between two events on the launch stream, mean per call).
+
+Work counts (algorithmic, implementation overhead excluded):
+  FLOPs = 4 * D * B * Hq * visible (query, key) pairs
+  bytes = 2 * D * (2 * B * Hkv * Skv + 2 * B * Hq * Sq)   (K, V read; Q read, O written)
+
+``cpu_baseline`` times the repo's CPU oracle (a numpy restatement of the
+reference's torch oracle, the reference's only CPU path) on a bounded sample
+of the same prefill workload, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--sweep]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "gqa-flash-attn-rtx3060_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "prefill TFLOP/s + decode µs & HBM GB/s, Llama-3.1-8B GQA shape, 1 MI355X"
+PEAK_BF16_TFLOPS = 2516.6  # dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 flop/CU/clk
+PEAK_HBM_GBS = 8000.0
+# Published reference number for this workload (RTX 3060, README.md:20,
+# benchmark/results/rtx3060_median5.json:31): prefill 16384 in 96.195 ms.
+REF_PREFILL_16K_MS = 96.195
+
+B, HQ, HKV, D = 1, 32, 8, 128
+PREFILL_S = 16384
+DECODE_S = 131072
+
+
+def visible_pairs(sq: int, skv: int, causal: bool = True) -> int:
+    """Unmasked (query, key) pairs per (batch, head): row i sees keys
+    [0, i + skv - sq], clipped to [0, skv) (bottom-right causal)."""
+    import numpy as np
+    if not causal:
+        return sq * skv
+    return int(np.clip(np.arange(sq, dtype=np.int64) + (skv - sq) + 1, 0, skv).sum())
+
+
+def flops(b, hq, sq, skv, d, causal=True) -> int:
+    return 4 * d * b * hq * visible_pairs(sq, skv, causal)
+
+
+def hbm_bytes(b, hq, hkv, sq, skv, d, elem=2) -> int:
+    return elem * d * (2 * b * hkv * skv + 2 * b * hq * sq)
+
+
+def _inputs(torch, b, hq, hkv, sq, skv, d, seed=0, n_kv_sets=1):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(b, hq, sq, d, device="cuda", generator=g).to(torch.bfloat16)
+    kvs = []
+    for _ in range(n_kv_sets):
+        k = torch.randn(b, hkv, skv, d, device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn(b, hkv, skv, d, device="cuda", generator=g).to(torch.bfloat16)
+        kvs.append((k, v))
+    return q, kvs
+
+
+def _time(torch, fn, steps, warmup):
+    """Mean ms per call of fn() over `steps` back-to-back calls, timed with
+    events on torch's current stream (the stream the kernels launch on)."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _gate(torch, gqa_flash_attn, q, k, v, rows=64, heads=(0, 1, 2, 3, 31)):
+    """Correctness gate on the timed inputs: the last `rows` query rows of a
+    few heads against a plain fp32 torch computation (max/mean abs error)."""
+    out = gqa_flash_attn(q, k, v, causal=True)
+    sq, skv, d = q.shape[2], k.shape[2], q.shape[3]
+    g = q.shape[1] // k.shape[1]
+    worst_max, sum_mean = 0.0, 0.0
+    for h in heads:
+        qq = q[0, h, sq - rows:].float().contiguous()
+        kt = k[0, h // g].float().t().contiguous()
+        s = torch.matmul(qq, kt) * d ** -0.5
+        qpos = torch.arange(sq - rows, sq, device="cuda") + (skv - sq)
+        s.masked_fill_(qpos[:, None] < torch.arange(skv, device="cuda")[None, :], float("-inf"))
+        ref = torch.matmul(torch.softmax(s, -1), v[0, h // g].float().contiguous())
+        diff = (out[0, h, sq - rows:].float() - ref).abs()
+        worst_max = max(worst_max, diff.max().item())
+        sum_mean += diff.mean().item()
+    return {"max_abs": worst_max, "mean_abs": sum_mean / len(heads), "rows_checked": rows * len(heads)}
+
+
+def _cpu_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
+        if n:
+            return int(max(n))
+    except Exception:
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(torch, q, k, v, budget_s=12.0):
+    """Time the CPU oracle on a bounded sample of the prefill workload: the
+    query group of kv head 0 (4 heads) for the last `n` rows, n doubled until
+    one run takes ~budget_s/4, then median of 3 runs."""
+    import numpy as np
+    from oracle.gqa_oracle import gqa_reference
+    sq, skv, d = q.shape[2], k.shape[2], q.shape[3]
+    g = q.shape[1] // k.shape[1]
+    qn = q[:, :g].float().cpu().numpy()
+    kn = k[:, :1].float().cpu().numpy()
+    vn = v[:, :1].float().cpu().numpy()
+    n = 64
+    while True:
+        rows = np.arange(sq - n, sq)
+        t0 = time.perf_counter()
+        gqa_reference(qn, kn, vn, True, rows=rows, dtype=np.float32)
+        dt = time.perf_counter() - t0
+        if dt > budget_s / 4 or n >= sq:
+            break
+        n = min(sq, n * 4 if dt < budget_s / 32 else n * 2)
+    times = [dt]
+    for _ in range(2):
+        t0 = time.perf_counter()
+        gqa_reference(qn, kn, vn, True, rows=rows, dtype=np.float32)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    work = 4 * d * g * sum(min(skv, int(r) + (skv - sq) + 1) for r in rows)
+    return {
+        "value": work / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": _cpu_threads(),
+        "kind": "port",
+        "sample": (f"numpy fp32 oracle, causal prefill S={sq}: q heads 0-{g - 1} (kv head 0), "
+                   f"last {n} query rows ({work / 1e9:.1f} GFLOP), median of 3 runs "
+                   f"({t:.2f} s each) on {_cpu_model()}"),
+        "seconds_per_run": t,
+    }
+
+
+def cpu_decode_baseline(torch, budget_runs=10):
+    """The reference's CPU config: decode B=1, Hq=32,
+    Hkv=8, D=128, seq_q=1, seq_kv=2048, N(0,1) from a CPU seed-0 generator."""
+    import numpy as np
+    from oracle.gqa_oracle import gqa_reference
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    q = torch.randn(1, 32, 1, 128, generator=gen).to(torch.bfloat16).float().numpy()
+    k = torch.randn(1, 8, 2048, 128, generator=gen).to(torch.bfloat16).float().numpy()
+    v = torch.randn(1, 8, 2048, 128, generator=gen).to(torch.bfloat16).float().numpy()
+    for _ in range(3):
+        gqa_reference(q, k, v, True)
+    ts = []
+    for _ in range(budget_runs):
+        t0 = time.perf_counter_ns()
+        gqa_reference(q, k, v, True)
+        ts.append(time.perf_counter_ns() - t0)
+    us = sorted(ts)[len(ts) // 2] / 1e3
+    return {"us": us, "gbs": hbm_bytes(1, 32, 8, 1, 2048, 128) / (us * 1e-6) / 1e9,
+            "cores": _cpu_threads(), "config": "decode B=1 Hq=32 Hkv=8 D=128 Sq=1 Skv=2048"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
+    ap.add_argument("--sweep", action="store_true", help="also time every BASELINE config")
+    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
+                    help="time one workload only (for profiling runs)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the attention path has no multi-GPU component.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from gqa_kernels import gqa_flash_attn
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+
+    result = {
+        "metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic N(0,1), seeded torch generator on the GPU",
+        "config": {"workload": f"causal GQA prefill B={B} Hq={HQ} Hkv={HKV} D={D} seq={PREFILL_S}",
+                   "global_batch": B, "seq_len": PREFILL_S, "parallelism": "single GPU"},
+    }
+
+    # ---------------- prefill (headline) ----------------
+    if args.only in (None, "prefill"):
+        q, kvs = _inputs(torch, B, HQ, HKV, PREFILL_S, PREFILL_S, D)
+        k, v = kvs[0]
+        gate = _gate(torch, gqa_flash_attn, q, k, v)
+        ms = _time(torch, lambda i: gqa_flash_attn(q, k, v, causal=True), args.steps, args.warmup)
+        fl = flops(B, HQ, PREFILL_S, PREFILL_S, D)
+        tflops = fl / (ms * 1e-3) / 1e12
+        result.update(value=tflops, ms_per_step=ms)
+        result["vs_baseline"] = REF_PREFILL_16K_MS / ms
+        result["vs_baseline_basis"] = ("speed-up over the reference's published RTX 3060 time for "
+                                       f"this workload ({REF_PREFILL_16K_MS} ms)")
+        result["gate"] = gate
+        result["roofline"] = {
+            "bound": "mfma", "kernel": "gqa_fwd_kernel", "achieved": tflops,
+            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS,
+            "traffic": None, "flops_per_launch": fl,
+            "note": "achieved = algorithmic FLOPs per launch / mean launch time (one launch per step)",
+        }
+        if not args.skip_cpu:
+            result["cpu_baseline"] = cpu_baseline(torch, q, k, v)
+        del q, k, v, kvs
+        torch.cuda.empty_cache()
+
+    # ---------------- decode ----------------
+    if args.only in (None, "decode"):
+        # Two K/V sets (1 GiB) so consecutive calls do not hit the 256 MB
+        # Infinity Cache with the previous call's data.
+        q, kvs = _inputs(torch, B, HQ, HKV, 1, DECODE_S, D, seed=1, n_kv_sets=2)
+        dsteps = max(args.steps * 5, 50)
+        ms = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % 2], causal=True), dsteps, args.warmup * 2)
+        by = hbm_bytes(B, HQ, HKV, 1, DECODE_S, D)
+        gbs = by / (ms * 1e-3) / 1e9
+        from gqa_kernels.dispatch import _cu_count, choose_route
+        route = choose_route(B, HQ, HKV, 1, DECODE_S, _cu_count(0))
+        result["decode"] = {
+            "workload": f"causal GQA decode B={B} Hq={HQ} Hkv={HKV} D={D} seq_q=1 seq_kv={DECODE_S}",
+            "us": ms * 1e3, "gbs": gbs, "steps": dsteps, "splits": route.splits,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "bytes_per_call": by,
+                         "note": "whole call (split first pass + combine), 2 rotating K/V sets"},
+        }
+        if not args.skip_cpu:
+            result["decode"]["cpu_baseline"] = cpu_decode_baseline(torch)
+        del q, kvs
+        torch.cuda.empty_cache()
+
+    if args.sweep:
+        result["sweep"] = sweep(torch, gqa_flash_attn)
+
+    if result["value"] is None and "decode" in result:
+        d = result["decode"]
+        result.update(value=d["gbs"], unit="GB/s", ms_per_step=d["us"] / 1e3)
+        result["config"]["workload"] = d["workload"]
+    print(json.dumps(result))
+    return 0
+
+
+def sweep(torch, gqa_flash_attn):
+    """Every BASELINE config: mean ms over 20 calls after 5 warm-ups."""
+    cfgs = [("prefill", 1, 32, 8, s, s) for s in (2048, 4096, 8192, 16384)]
+    cfgs += [("decode", 1, 32, 8, 1, s) for s in (8192, 32768, 131072)]
+    cfgs += [("chunked", 4, 32, 8, 512, 8192), ("70b", 16, 64, 8, 4, 32768)]
+    rows = []
+    for name, b, hq, hkv, sq, skv in cfgs:
+        by1 = hbm_bytes(b, hq, hkv, sq, skv, D)
+        nset = 1 if by1 > 600e6 else max(2, math.ceil(600e6 / by1))
+        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, D, n_kv_sets=min(nset, 8))
+        ms = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % len(kvs)], causal=True), 20, 5)
+        fl = flops(b, hq, sq, skv, D)
+        rows.append({"workload": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv,
+                     "ms": ms, "tflops": fl / (ms * 1e-3) / 1e12,
+                     "gbs": by1 / (ms * 1e-3) / 1e9})
+        del q, kvs
+        torch.cuda.empty_cache()
+    return rows
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,174 @@
+"""Host-side logic and the C ABI, without a GPU (CPU only).
+
+* the library loads and exports every entry point declared in
+  include/gqa_attn.h, with the ctypes signatures matching the header;
+* argument validation in the C launchers (error codes are returned before any
+  HIP call, so they are testable here);
+* the dispatch rule (single-pass vs split-KV, split count for 256 CUs);
+* the Python asserts of reference gqa_kernels/dispatch.py:30-33.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "gqa_attn.h"
+
+
+def _declared():
+    """(name, n_params) of every function declared in the public header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b([a-z_0-9]+)\s*\(([^;{]*?)\)\s*;", text):
+        name, params = m.group(1), m.group(2).strip()
+        if not name.startswith("gqa_"):
+            continue
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from gqa_kernels import _lib
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = set(_declared())
+    assert {"gqa_fwd_launch", "gqa_split_first_launch", "gqa_split_reduce_launch",
+            "gqa_split_workspace_bytes", "gqa_device_cu_count", "gqa_strerror",
+            "gqa_abi_version"} <= names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from gqa_kernels import _lib
+    for name, nparams in _declared().items():
+        assert hasattr(lib, name), f"libgqa_hip.so lacks {name}"
+        assert name in _lib.SIGNATURES, f"no ctypes signature for {name}"
+        assert len(_lib.SIGNATURES[name][1]) == nparams, name
+
+
+def test_abi_version_and_strerror(lib):
+    from gqa_kernels import _lib
+    assert lib.gqa_abi_version() == _lib.ABI_VERSION
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -99):
+        msg = lib.gqa_strerror(code)
+        assert isinstance(msg, bytes) and msg
+    assert b"head_dim" in lib.gqa_strerror(-2)
+
+
+def test_workspace_bytes(lib):
+    from gqa_kernels.gqa_split import workspace_bytes
+    for args in ((1, 32, 1, 128, 128), (16, 64, 4, 128, 8), (2, 8, 3, 64, 7)):
+        assert lib.gqa_split_workspace_bytes(*args) == workspace_bytes(*args)
+        B, H, S, D, SP = args
+        assert workspace_bytes(*args) == B * H * S * SP * (D + 2) * 4
+    assert lib.gqa_split_workspace_bytes(0, 32, 1, 128, 8) == 0
+
+
+_S4 = (ctypes.c_int64 * 4)(8 * 128 * 128, 128 * 128, 128, 1)
+_BAD = (ctypes.c_int64 * 4)(8 * 128 * 128, 128 * 128, 128, 2)
+_FAKE = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("args,code", [
+    (dict(Hq=32, Hkv=6), -1),       # heads not divisible
+    (dict(D=96), -2),               # head_dim
+    (dict(dtype=7), -3),            # dtype
+    (dict(stride=_BAD), -4),        # last-dim stride
+    (dict(Hq=256, Hkv=1), -6),      # group larger than one packed tile
+    (dict(Sq=-1), -1),
+])
+def test_fwd_launch_validation(lib, args, code):
+    p = dict(Hq=32, Hkv=8, D=128, dtype=0, stride=_S4, Sq=128)
+    p.update(args)
+    st = p["stride"]
+    rc = lib.gqa_fwd_launch(_FAKE, st, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4,
+                            1, p["Hq"], p["Hkv"], p["Sq"], 128, p["D"], 0.1275, 1, p["dtype"], None)
+    assert rc == code
+
+
+def test_empty_launches_are_noops(lib):
+    # batch 0 / seq_q 0: nothing to do, no HIP call, success.
+    assert lib.gqa_fwd_launch(None, _S4, None, _S4, None, _S4, None, _S4,
+                              0, 32, 8, 16, 16, 128, 0.1, 1, 0, None) == 0
+    assert lib.gqa_fwd_launch(None, _S4, None, _S4, None, _S4, None, _S4,
+                              1, 32, 8, 0, 16, 128, 0.1, 1, 0, None) == 0
+
+
+def test_split_launch_validation(lib):
+    f = lib.gqa_split_first_launch
+    assert f(_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, 0, 1, 32, 8, 1, 4096, 128, 0.1, 1, 0, None) == -5
+    assert f(_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, 2048, 1, 32, 8, 1, 4096, 128, 0.1, 1, 0, None) == -5
+    assert f(_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, None, 8, 1, 32, 8, 1, 4096, 128, 0.1, 1, 0, None) == -7
+    misaligned = ctypes.c_void_p((1 << 20) + 4)
+    assert f(_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, misaligned, 8, 1, 32, 8, 1, 4096, 128, 0.1, 1, 0,
+             None) == -4
+    r = lib.gqa_split_reduce_launch
+    assert r(_FAKE, 8, _FAKE, _S4, 1, 32, 1, 80, 0, None) == -2
+    assert r(_FAKE, 0, _FAKE, _S4, 1, 32, 1, 128, 0, None) == -5
+    assert r(_FAKE, 8, _FAKE, _BAD, 1, 32, 1, 128, 0, None) == -4
+
+
+# ---------------------------------------------------------------------------
+# Dispatch rule
+# ---------------------------------------------------------------------------
+def test_route_baseline_configs():
+    from gqa_kernels.dispatch import choose_route
+    cu = 256
+    # prefill: single pass, 128 packed rows (32 positions x 4 heads) per workgroup
+    r = choose_route(1, 32, 8, 16384, 16384, cu)
+    assert r.kind == "single" and r.workgroups == 512 * 8
+    # decode 131072: split to 4 workgroups per CU
+    r = choose_route(1, 32, 8, 1, 131072, cu)
+    assert r.kind == "split" and r.splits == 128 and r.workgroups == 1024
+    # decode 8192: limited by the minimum chunk (256 keys)
+    r = choose_route(1, 32, 8, 1, 8192, cu)
+    assert r.kind == "split" and r.splits == 32
+    # 70B multi-token decode: 32 packed rows per kv head, 128 (b, kv head) pairs
+    r = choose_route(16, 64, 8, 4, 32768, cu)
+    assert r.kind == "split" and r.splits == 8 and r.workgroups == 1024
+    # chunked prefill: single pass
+    assert choose_route(4, 32, 8, 512, 8192, cu).kind == "single"
+    # reference decode cases below the split threshold stay single-pass
+    assert choose_route(1, 32, 8, 1, 512, cu).kind == "single"
+
+
+def test_route_properties():
+    from gqa_kernels.dispatch import SPLIT_MIN_TILES, SPLIT_TILE, choose_route
+    for skv in (1024, 1500, 4096, 65536, 1 << 20):
+        for b in (1, 2, 8, 64):
+            for cu in (80, 256):
+                r = choose_route(b, 32, 8, 1, skv, cu)
+                assert r.kind == "split"
+                assert r.splits & (r.splits - 1) == 0  # power of two
+                assert r.splits == 1 or -(-skv // r.splits) >= SPLIT_MIN_TILES * SPLIT_TILE
+                # never more splits than needed for 4 workgroups per CU
+                assert r.splits == 1 or (r.workgroups // 2) < 4 * cu
+
+
+# ---------------------------------------------------------------------------
+# Python asserts (reference dispatch.py:30-33), tripped on CPU tensors
+# ---------------------------------------------------------------------------
+def test_asserts_on_cpu():
+    from gqa_kernels import gqa_flash_attn
+    q = torch.zeros(1, 32, 4, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 8, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="divisible"):
+        gqa_flash_attn(q, torch.zeros(1, 6, 4, 128, dtype=torch.bfloat16),
+                       torch.zeros(1, 6, 4, 128, dtype=torch.bfloat16))
+    with pytest.raises(AssertionError, match="head_dim"):
+        gqa_flash_attn(q[..., :96], k[..., :96], k[..., :96])
+    with pytest.raises(AssertionError):
+        gqa_flash_attn(q, k, k)  # CPU tensors: is_cuda assert
+
+
+def test_package_exports():
+    import gqa_kernels
+    assert gqa_kernels.__all__ == ["gqa_flash_attn"]
+    assert gqa_kernels.__version__ == "0.1.0"
