@@ -133,11 +133,26 @@ template <int D> struct SubTileRegs {
 
 // Load keys [key0, key0 + 64) of one (b, kv head) into registers; rows at or
 // beyond `key_lim` read as zero.  kbase/vbase point at key 0 of the head;
-// kss/vss are the key strides in elements.
+// kss/vss are the key strides in elements.  A tile that lies entirely below
+// key_lim (all but the last) takes the unpredicated path.
 template <int D, typename T>
 __device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kbase,
                                     const T* __restrict__ vbase, int64_t kss, int64_t vss,
                                     int key0, int key_lim, int t) {
+  const int d4 = t % (D / 4), kg = t / (D / 4);
+  constexpr int KPT = SubTileRegs<D>::KPT;
+  if (key0 + 64 <= key_lim) {
+#pragma unroll
+    for (int j = 0; j < SubTileRegs<D>::KCH; ++j) {
+      const int ci = t + 256 * j;
+      const int r = ci / (D / 8), cd = ci % (D / 8);
+      R.k[j] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(key0 + r) * kss + cd * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+      R.v[j] = *reinterpret_cast<const u32x2*>(vbase + (int64_t)(key0 + kg * KPT + j) * vss + d4 * 4);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < SubTileRegs<D>::KCH; ++j) {
     const int ci = t + 256 * j;
@@ -147,10 +162,9 @@ __device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kba
     if (key < key_lim) x = *reinterpret_cast<const u32x4*>(kbase + (int64_t)key * kss + cd * 8);
     R.k[j] = x;
   }
-  const int d4 = t % (D / 4), kg = t / (D / 4);
 #pragma unroll
-  for (int j = 0; j < SubTileRegs<D>::KPT; ++j) {
-    const int key = key0 + kg * SubTileRegs<D>::KPT + j;
+  for (int j = 0; j < KPT; ++j) {
+    const int key = key0 + kg * KPT + j;
     u32x2 x = {0u, 0u};
     if (key < key_lim) x = *reinterpret_cast<const u32x2*>(vbase + (int64_t)key * vss + d4 * 4);
     R.v[j] = x;
@@ -220,6 +234,57 @@ __device__ inline void pv_block(const char* __restrict__ lds, const u32x4 p[2], 
       acc[db] = Elem<DT>::mfma(a, p[kk], acc[db]);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Online softmax over one 32-key S^T block (16 values per lane; the two lane
+// halves hold the other 16 keys of the same row), exp2 domain.
+//
+// Lazy rescaling: the reference point m_ref of a row is only raised when the
+// block's max exceeds it by more than kRescaleLog2 (log2 units); otherwise the
+// probabilities are computed against the stale m_ref and may reach
+// 2^kRescaleLog2, which bf16/fp16 P and fp32 l/acc hold exactly as well.  The
+// decision is wave-uniform, so in steady state the O accumulators are not
+// touched by the VALU at all.  The result o = acc / l is unchanged (both are
+// relative to the same m_ref).  A row whose m_ref is still -inf uses 0 as the
+// reference, so a fully masked block contributes p = 0, never NaN.
+// ---------------------------------------------------------------------------
+constexpr float kRescaleLog2 = 8.0f;
+
+template <int DT, int NACC>
+__device__ inline void softmax_block(f32x16& s, float& m_ref, float& l_run, f32x16 (&acc)[NACC],
+                                     float c, u32x4 (&pk)[2]) {
+  using E = Elem<DT>;
+  float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+  for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[v]);
+  mx = xhalf_max(mx);
+  const bool grow = (mx - m_ref) * c > kRescaleLog2;  // false for NaN (both -inf)
+  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    const float m_new = fmaxf(m_ref, mx);
+    const float m_new_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = fast_exp2((m_ref - m_new_use) * c);
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < NACC; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
+    m_ref = m_new;
+  }
+  const float m_use = (m_ref == -__builtin_inff()) ? 0.f : m_ref;
+  const float nmc = -m_use * c;
+  float pv[16];
+  float rs = 0.f;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    pv[v] = fast_exp2(__builtin_fmaf(s[v], c, nmc));
+    rs += pv[v];
+  }
+  l_run += rs;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pk[kk][e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
 }
 
 // ---------------------------------------------------------------------------

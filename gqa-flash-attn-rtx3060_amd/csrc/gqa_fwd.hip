@@ -18,7 +18,7 @@
 namespace gqa {
 
 template <int DT, int D>
-__global__ __launch_bounds__(256) void gqa_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_fwd_kernel(FwdParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
   using ST = SubTile<D>;
@@ -89,61 +89,23 @@ __global__ __launch_bounds__(256) void gqa_fwd_kernel(FwdParams p) {
     const bool has_next = it + 1 < ntiles;
     if (has_next) load_subtile<D, T>(R, kbase, vbase, p.k.ss, p.v.ss, key0 + kFwdTileKeys, dm.Skv, t);
 
-    f32x16 s[2];
-    s[0] = qk_block<DT, D>(cur, qreg, 0, lane);
-    s[1] = qk_block<DT, D>(cur, qreg, 1, lane);
-
     const bool need_mask =
         (key0 + kFwdTileKeys > dm.Skv) || (dm.causal && key0 + kFwdTileKeys - 1 > qpos_lo);
-    if (need_mask) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < 2; ++mb) {
+      f32x16 s = qk_block<DT, D>(cur, qreg, mb, lane);
+      if (need_mask) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = key0 + 32 * mb + key_of(v, hh);
-          if (key >= dm.Skv || (dm.causal && key > qpos)) s[mb][v] = -__builtin_inff();
+          const bool off = key >= dm.Skv || (dm.causal && key > qpos);
+          s[v] = off ? -__builtin_inff() : s[v];
         }
-    }
-
-    // Online softmax over this tile (row = lane % 32; the two lane halves
-    // hold disjoint keys of the same row).
-    float mx = s[0][0];
-#pragma unroll
-    for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
-#pragma unroll
-    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
-    mx = xhalf_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = fast_exp2((m_run - m_use) * c);
-    const float nmc = -m_use * c;
-    float rs = 0.f;
-    u32x4 pk[2][2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      float pv[16];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        pv[v] = fast_exp2(__builtin_fmaf(s[mb][v], c, nmc));
-        rs += pv[v];
       }
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        u32x4 x;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
-        pk[mb][kk] = x;
-      }
+      u32x4 pk[2];
+      softmax_block<DT, D / 32>(s, m_run, l_run, acc, c, pk);
+      pv_block<DT, D>(cur, pk, acc, mb, lane);
     }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
-
-    pv_block<DT, D>(cur, pk[0], acc, 0, lane);
-    pv_block<DT, D>(cur, pk[1], acc, 1, lane);
 
     if (has_next) store_subtile<D>(smem + ((it + 1) & 1) * ST::kBytes, R, t);
     __syncthreads();
