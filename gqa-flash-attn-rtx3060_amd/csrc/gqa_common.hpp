@@ -237,6 +237,115 @@ __device__ inline void pv_block(const char* __restrict__ lds, const u32x4 p[2], 
 }
 
 // ---------------------------------------------------------------------------
+// Single-pass LDS tile (64 keys x D), double-buffered.
+//
+// K part: row-major, 16-byte chunks, chunk cd of row r stored at cd ^ gk(r).
+// K is written by direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes
+// write 1 KiB contiguous), so the swizzle is applied on the global side: the
+// lane that lands on physical chunk pc of row r fetches chunk pc ^ gk(r).
+// gk is chosen so that the S^T A-operand reads (row pi(i), chunk 2ks+h) hit
+// 16 distinct 16-byte bank groups in every 16 consecutive lanes and 8 distinct
+// groups modulo 128 bytes in every 8 lanes (conflict-free whether the LDS
+// serves 8 or 16 lanes of a 128-bit read per cycle).  With that gk,
+// gk(pi(i)) = i & (CPR - 1): the read chunk of lane i is simply (2ks+h) ^ i.
+//
+// V part: transposed [d][key], chunks of 8 keys, chunk c of row d stored at
+// c ^ f(d), f(d) = (d + d/8) & 7 (the same layout as SubTile).
+// ---------------------------------------------------------------------------
+template <int D> struct FwdTile {
+  static constexpr int kKeys = 64;
+  static constexpr int CPR = D / 8;  // 16-byte chunks per K row
+  static constexpr int kKBytes = kKeys * D * 2;
+  static constexpr int kVBytes = D * kKeys * 2;
+  static constexpr int kBytes = kKBytes + kVBytes;
+
+  __device__ static constexpr int gk(int r) {
+    return CPR == 16 ? ((r & 3) | (((r >> 3) & 1) << 2) | (((r >> 2) & 1) << 3))
+                     : ((r & 3) | (((r >> 3) & 1) << 2));
+  }
+  __device__ static constexpr int f0(int i) { return (i + (i >> 3)) & 7; }
+};
+
+// Buffer resource over `bytes` bytes at `base` (raw buffer, stride 0).
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// Issue the direct-to-LDS loads (buffer_load_dwordx4 ... lds) of K rows
+// [key0, key0 + 64) into the K part of an FwdTile; the destination is
+// wave-uniform and each instruction covers 64 chunks.  Rows at or beyond
+// nrows_valid are not loaded (their LDS content is stale and every key there
+// is masked before use).  rk: descriptor of this (b, kv head)'s K rows;
+// k0b = key0 * key stride in bytes; koff: this lane's byte offset (its row in
+// the instruction times the key stride + its swizzled chunk).
+template <int D>
+__device__ inline void issue_k_dma(char* __restrict__ lds_tile, __amdgpu_buffer_rsrc_t rk, uint32_t k0b,
+                                   uint32_t kssb, uint32_t koff, int lane_row0, int nrows_valid, int wave) {
+  using FT = FwdTile<D>;
+  constexpr int RPI = 64 / FT::CPR;                // rows per instruction
+  constexpr int NI = (FT::kKeys * FT::CPR) / 256;  // instructions per thread
+  typedef __attribute__((address_space(3))) void lds_void;
+  const bool full = nrows_valid >= FT::kKeys;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int step = j * 4 + wave;  // instruction index within the tile
+    lds_void* l = (lds_void*)(lds_tile + step * 1024);
+    const uint32_t so = k0b + (uint32_t)(step * RPI) * kssb;
+    if (full || lane_row0 + step * RPI < nrows_valid)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, l, 16, koff, so, 0, 0);
+  }
+}
+
+// V staging for one 64-key tile: thread owns keys [KPT*kg, KPT*kg + KPT) x
+// d [4*d4, 4*d4 + 4), d4 = t % (D/4), kg = t / (D/4), KPT = D/16.
+template <int D> struct VRegs {
+  static constexpr int KPT = D / 16;
+  u32x2 v[KPT];
+};
+
+// rv: descriptor of this (b, kv head)'s V rows; k0b = key0 * key stride in
+// bytes; voff = kg*KPT*vssb + 8*d4; rows >= nrows_valid read as 0.
+template <int D>
+__device__ inline void load_v_regs(VRegs<D>& R, __amdgpu_buffer_rsrc_t rv, uint32_t k0b, uint32_t vssb,
+                                   uint32_t voff, int row0, int nrows_valid) {
+  constexpr int KPT = VRegs<D>::KPT;
+  if (nrows_valid >= 64) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) R.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, k0b + j * vssb, 0);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    u32x2 x = {0u, 0u};
+    if (row0 + j < nrows_valid) x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, k0b + j * vssb, 0);
+    R.v[j] = x;
+  }
+}
+
+template <int D>
+__device__ inline void store_v_lds(char* __restrict__ lds_tile, const VRegs<D>& R, int t) {
+  using FT = FwdTile<D>;
+  constexpr int KPT = VRegs<D>::KPT;
+  const int d4 = t % (D / 4), kg = t / (D / 4);
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) {
+    const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+    uint32_t w[KPT / 2];
+#pragma unroll
+    for (int i = 0; i < KPT / 2; ++i) w[i] = __builtin_amdgcn_perm(R.v[2 * i + 1][dd >> 1], R.v[2 * i][dd >> 1], sel);
+    const int d = 4 * d4 + dd;
+    const int f = (d + (d >> 3)) & 7;
+    if constexpr (KPT == 8) {
+      u32x4 o = {w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(lds_tile + FT::kKBytes + d * 128 + ((kg ^ f) << 4)) = o;
+    } else {
+      u32x2 o = {w[0], w[1]};
+      *reinterpret_cast<u32x2*>(lds_tile + FT::kKBytes + d * 128 + (((kg >> 1) ^ f) << 4) + ((kg & 1) << 3)) = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Online softmax over one 32-key S^T block (16 values per lane; the two lane
 // halves hold the other 16 keys of the same row), exp2 domain.
 //

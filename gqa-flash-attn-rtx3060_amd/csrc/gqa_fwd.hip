@@ -12,6 +12,8 @@
 // flight while the current one is computed.  Causal: the key loop stops at
 // the workgroup's last visible key (gqa_fwd.py:70-73) and masks only the
 // tiles that cross the diagonal or the end of the keys.
+#include <type_traits>
+
 #include "gqa_common.hpp"
 #include "gqa_params.hpp"
 
@@ -21,11 +23,19 @@ template <int DT, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_fwd_kernel(FwdParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
-  using ST = SubTile<D>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * ST::kBytes];
+  using FT = FwdTile<D>;
+  constexpr int CPR = FT::CPR;
+  constexpr int RPI = 64 / CPR;
+  constexpr int KPT = VRegs<D>::KPT;
+  // Two separate arrays (not one array of two halves): the compiler can then
+  // tell the DMA target of the next tile from the buffer being read, and does
+  // not wait for the in-flight loads before the reads of the current tile.
+  __shared__ __attribute__((aligned(1024))) char smem0[FT::kBytes];
+  __shared__ __attribute__((aligned(1024))) char smem1[FT::kBytes];
 
   const Dims& dm = p.dm;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;  // wave-uniform (SGPR), 0..3
   const int i = lane & 31, hh = lane >> 5;
 
   // Work item: heavy (late) query blocks first under causal, and every XCD
@@ -63,11 +73,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int kv_end = dm.Skv;
   if (dm.causal) kv_end = min(dm.Skv, pos_hi + (dm.Skv - dm.Sq) + 1);
   kv_end = max(kv_end, 0);
-  const int ntiles = (kv_end + kFwdTileKeys - 1) / kFwdTileKeys;
+  const int ntiles = (kv_end + FT::kKeys - 1) / FT::kKeys;
   const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
 
-  const T* kbase = static_cast<const T*>(p.k.ptr) + (int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh;
-  const T* vbase = static_cast<const T*>(p.v.ptr) + (int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh;
+  // Global side: buffer descriptors over this (b, kv head)'s K and V rows
+  // (the host guarantees seq_kv * key stride * 2 < 2^31), per-lane offsets.
+  const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
+  const char* kbh = static_cast<const char*>(p.k.ptr) + 2 * ((int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh);
+  const char* vbh = static_cast<const char*>(p.v.ptr) + 2 * ((int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbh, 0x7fffffffu);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, 0x7fffffffu);
+  const int lrow = lane / CPR;
+  const uint32_t koff =
+      (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ FT::gk((wave * RPI + lrow) & 15));
+  const int d4 = t % (D / 4), kg = t / (D / 4);
+  const uint32_t voff = (uint32_t)(kg * KPT * vssb) + 8u * (uint32_t)d4;
+
+  // LDS side: per-lane read offsets (the tile buffer, the 32-key block and
+  // the 32-row d block are immediate offsets on top of these).  The masks are
+  // no-ops on the values; they give the compiler known bounds, so it can prove
+  // that reads of one buffer never touch the other and does not wait for the
+  // next tile's in-flight loads.
+  constexpr uint32_t kKMask = (FT::kKBytes / 2 - 1) & ~15u;  // rows 0..31 of K
+  constexpr uint32_t kVMask = (FT::kBytes - 1) & ~15u;
+  uint32_t ka[D / 16];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
+  uint32_t va[2][2];
+  {
+    const int z = hh ^ FT::f0(i);
+#pragma unroll
+    for (int mp = 0; mp < 2; ++mp)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        va[mp][kk] = (uint32_t)(FT::kKBytes + 128 * i + 16 * ((4 * mp + 2 * kk) ^ z)) & kVMask;
+  }
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -76,40 +117,66 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float l_run = 0.f;
   const float c = dm.c;
 
-  SubTileRegs<D> R;
+  VRegs<D> R;
   if (ntiles > 0) {
-    load_subtile<D, T>(R, kbase, vbase, p.k.ss, p.v.ss, 0, dm.Skv, t);
-    store_subtile<D>(smem, R, t);
+    const int nv = min(FT::kKeys, dm.Skv);
+    issue_k_dma<D>(smem0, rk, 0u, kssb, koff, lrow, nv, wave);
+    load_v_regs<D>(R, rv, 0u, vssb, voff, kg * KPT, nv);
+    store_v_lds<D>(smem0, R, t);
   }
   __syncthreads();
 
-  for (int it = 0; it < ntiles; ++it) {
-    const char* cur = smem + (it & 1) * ST::kBytes;
-    const int key0 = it * kFwdTileKeys;
+  auto step = [&](auto bufc, int it) {
+    constexpr int BUF = decltype(bufc)::value;
+    const char* cur = BUF ? smem1 : smem0;
+    char* nxt = BUF ? smem0 : smem1;
+    const int key0 = it * FT::kKeys;
     const bool has_next = it + 1 < ntiles;
-    if (has_next) load_subtile<D, T>(R, kbase, vbase, p.k.ss, p.v.ss, key0 + kFwdTileKeys, dm.Skv, t);
+    if (has_next) {
+      const int k1 = key0 + FT::kKeys;
+      const int nv = min(FT::kKeys, dm.Skv - k1);
+      issue_k_dma<D>(nxt, rk, (uint32_t)k1 * kssb, kssb, koff, lrow, nv, wave);
+      load_v_regs<D>(R, rv, (uint32_t)k1 * vssb, vssb, voff, kg * KPT, nv);
+    }
 
-    const bool need_mask =
-        (key0 + kFwdTileKeys > dm.Skv) || (dm.causal && key0 + kFwdTileKeys - 1 > qpos_lo);
+    const bool need_mask = (key0 + FT::kKeys > dm.Skv) || (dm.causal && key0 + FT::kKeys - 1 > qpos_lo);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      f32x16 s = qk_block<DT, D>(cur, qreg, mb, lane);
+      f32x16 sc = {};
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(cur + mb * 32 * (2 * D) + ka[ks]);
+        sc = E::mfma(a, qreg[ks], sc);
+      }
       if (need_mask) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = key0 + 32 * mb + key_of(v, hh);
           const bool off = key >= dm.Skv || (dm.causal && key > qpos);
-          s[v] = off ? -__builtin_inff() : s[v];
+          sc[v] = off ? -__builtin_inff() : sc[v];
         }
       }
       u32x4 pk[2];
-      softmax_block<DT, D / 32>(s, m_run, l_run, acc, c, pk);
-      pv_block<DT, D>(cur, pk, acc, mb, lane);
+      softmax_block<DT, D / 32>(sc, m_run, l_run, acc, c, pk);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(cur + 4096 * db + va[mb ^ (db & 1)][kk]);
+          acc[db] = E::mfma(a, pk[kk], acc[db]);
+        }
     }
 
-    if (has_next) store_subtile<D>(smem + ((it + 1) & 1) * ST::kBytes, R, t);
+    if (has_next) store_v_lds<D>(nxt, R, t);
     __syncthreads();
+  };
+
+  int it = 0;
+  for (; it + 2 <= ntiles; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    step(std::integral_constant<int, 1>{}, it + 1);
   }
+  if (it < ntiles) step(std::integral_constant<int, 0>{}, it);
 
   // Epilogue: o = acc / l (0/0 = NaN for a row with no visible key, as the
   // reference's acc / l_i at gqa_fwd.py:106).
