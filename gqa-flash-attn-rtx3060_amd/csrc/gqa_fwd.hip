@@ -140,24 +140,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     const bool need_mask = (key0 + FT::kKeys > dm.Skv) || (dm.causal && key0 + FT::kKeys - 1 > qpos_lo);
+    // Issue both S^T chains first: block 1's MFMAs then execute while the
+    // softmax of block 0 runs on the VALU, and PV of block 0 overlaps the
+    // softmax of block 1.
+    f32x16 sc[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      f32x16 sc = {};
+      sc[mb] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(cur + mb * 32 * (2 * D) + ka[ks]);
-        sc = E::mfma(a, qreg[ks], sc);
+        sc[mb] = E::mfma(a, qreg[ks], sc[mb]);
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
       if (need_mask) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = key0 + 32 * mb + key_of(v, hh);
           const bool off = key >= dm.Skv || (dm.causal && key > qpos);
-          sc[v] = off ? -__builtin_inff() : sc[v];
+          sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
       }
       u32x4 pk[2];
-      softmax_block<DT, D / 32>(sc, m_run, l_run, acc, c, pk);
+      softmax_block<DT, D / 32>(sc[mb], m_run, l_run, acc, c, pk);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -165,6 +173,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const u32x4 a = *reinterpret_cast<const u32x4*>(cur + 4096 * db + va[mb ^ (db & 1)][kk]);
           acc[db] = E::mfma(a, pk[kk], acc[db]);
         }
+      if (mb == 0) __builtin_amdgcn_sched_barrier(0);
     }
 
     if (has_next) store_v_lds<D>(nxt, R, t);
