@@ -6,6 +6,8 @@
 // 16-byte aligned rows).  Nothing here allocates device memory.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "../../include/gqa_attn.h"
 #include "gqa_params.hpp"
 
@@ -123,6 +125,49 @@ int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void*
   p.splits = splits;
   p.chunk = (seq_kv + splits - 1) / splits;
   p.n_rblk = (G * seq_q + 31) / 32;
+  p.counters = nullptr;
+  p.o = TensorRef{nullptr, 0, 0, 0};
+  return to_code(gqa::launch_split_first(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+size_t gqa_split_counters_count(int batch, int num_heads, int num_kv_heads, int seq_q) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || seq_q <= 0 || num_heads % num_kv_heads) return 0;
+  const size_t G = (size_t)(num_heads / num_kv_heads);
+  return (size_t)batch * num_kv_heads * ((G * seq_q + 31) / 32);
+}
+
+int gqa_split_fused_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                           const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
+                           float* workspace, int* counters, int splits, int batch, int num_heads,
+                           int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2, int causal,
+                           int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
+  if (rc) return rc;
+  if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (workspace == nullptr || counters == nullptr) return GQA_E_NULL;
+  if ((int64_t)std::min(32, (num_heads / num_kv_heads) * seq_q) * splits > gqa::kFusedMaxRowSplitsHost)
+    return GQA_E_SPLITS;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || (reinterpret_cast<uintptr_t>(counters) & 3u) != 0)
+    return GQA_E_STRIDE;
+  if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
+  if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
+
+  const int G = num_heads / num_kv_heads;
+  gqa::SplitParams p;
+  p.q = ref(q, q_stride);
+  p.k = ref(k, k_stride);
+  p.v = ref(v, v_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, G, scale_log2, causal ? 1 : 0};
+  const size_t rows = (size_t)batch * num_heads * seq_q * splits;
+  p.ws_acc = workspace;
+  p.ws_m = workspace + rows * head_dim;
+  p.ws_l = p.ws_m + rows;
+  p.splits = splits;
+  p.chunk = (seq_kv + splits - 1) / splits;
+  p.n_rblk = (G * seq_q + 31) / 32;
+  p.counters = counters;
+  p.o = ref(o, o_stride);
   return to_code(gqa::launch_split_first(p, dtype, static_cast<hipStream_t>(stream)));
 }
 

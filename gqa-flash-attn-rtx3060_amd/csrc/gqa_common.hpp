@@ -131,11 +131,25 @@ template <int D> struct SubTileRegs {
   u32x2 v[KPT];
 };
 
+// 16- and 8-byte global loads; kStream selects the non-temporal form
+// (global_load ... nt), which streams data that is read exactly once at a
+// markedly higher rate than cached loads on MI355X HBM.
+template <bool kStream>
+__device__ inline u32x4 ld16(const void* p) {
+  if constexpr (kStream) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return *reinterpret_cast<const u32x4*>(p);
+}
+template <bool kStream>
+__device__ inline u32x2 ld8(const void* p) {
+  if constexpr (kStream) return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+  return *reinterpret_cast<const u32x2*>(p);
+}
+
 // Load keys [key0, key0 + 64) of one (b, kv head) into registers; rows at or
 // beyond `key_lim` read as zero.  kbase/vbase point at key 0 of the head;
 // kss/vss are the key strides in elements.  A tile that lies entirely below
 // key_lim (all but the last) takes the unpredicated path.
-template <int D, typename T>
+template <int D, typename T, bool kStream = false>
 __device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kbase,
                                     const T* __restrict__ vbase, int64_t kss, int64_t vss,
                                     int key0, int key_lim, int t) {
@@ -146,11 +160,10 @@ __device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kba
     for (int j = 0; j < SubTileRegs<D>::KCH; ++j) {
       const int ci = t + 256 * j;
       const int r = ci / (D / 8), cd = ci % (D / 8);
-      R.k[j] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(key0 + r) * kss + cd * 8);
+      R.k[j] = ld16<kStream>(kbase + (int64_t)(key0 + r) * kss + cd * 8);
     }
 #pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      R.v[j] = *reinterpret_cast<const u32x2*>(vbase + (int64_t)(key0 + kg * KPT + j) * vss + d4 * 4);
+    for (int j = 0; j < KPT; ++j) R.v[j] = ld8<kStream>(vbase + (int64_t)(key0 + kg * KPT + j) * vss + d4 * 4);
     return;
   }
 #pragma unroll
@@ -159,14 +172,14 @@ __device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kba
     const int r = ci / (D / 8), cd = ci % (D / 8);
     const int key = key0 + r;
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (key < key_lim) x = *reinterpret_cast<const u32x4*>(kbase + (int64_t)key * kss + cd * 8);
+    if (key < key_lim) x = ld16<kStream>(kbase + (int64_t)key * kss + cd * 8);
     R.k[j] = x;
   }
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const int key = key0 + kg * KPT + j;
     u32x2 x = {0u, 0u};
-    if (key < key_lim) x = *reinterpret_cast<const u32x2*>(vbase + (int64_t)key * vss + d4 * 4);
+    if (key < key_lim) x = ld8<kStream>(vbase + (int64_t)key * vss + d4 * 4);
     R.v[j] = x;
   }
 }
@@ -394,6 +407,20 @@ __device__ inline void softmax_block(f32x16& s, float& m_ref, float& l_run, f32x
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
     for (int e = 0; e < 4; ++e) pk[kk][e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
+}
+
+// ---------------------------------------------------------------------------
+// Device-coherent (agent scope) 32-bit stores and loads.  On gfx950 they are
+// plain global stores/loads with sc1 set: they write through to / read from
+// the point where all XCDs are coherent, so data passed between workgroups
+// of one launch needs no L2 write-back or invalidate (which a release or
+// acquire fence at agent scope performs for the whole L2 of the XCD).
+// ---------------------------------------------------------------------------
+__device__ inline void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------

@@ -37,6 +37,11 @@ struct SplitParams {
   int splits;
   int chunk;   // ceil(Skv / splits)
   int n_rblk;  // ceil(G * Sq / 32)
+  // Fused combine (optional): when counters != nullptr, the last workgroup of
+  // each (b, kv head, row block) to finish combines the splits into o.
+  // counters: B * Hkv * n_rblk ints, zero on entry, left zero on exit.
+  int* counters;
+  TensorRef o;
 };
 
 // Split-KV combine: one workgroup per (b, q head, query row).
@@ -53,9 +58,12 @@ constexpr int kFwdRows = 128;
 // Keys per single-pass LDS tile, and per split-KV LDS tile.
 constexpr int kFwdTileKeys = 64;
 constexpr int kSplitTileKeys = 128;
+// The fused combine stages (valid rows of a 32-row block) x splits values in
+// LDS; above this the separate combine kernel is used.
+constexpr int kFusedMaxRowSplitsHost = 4096;
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream);
-hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream);
+hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream);  // fused if p.counters
 hipError_t launch_split_reduce(const ReduceParams& p, int dtype, hipStream_t stream);
 
 }  // namespace gqa

@@ -23,13 +23,108 @@
 
 namespace gqa {
 
+// Largest (valid rows x splits) the in-kernel combine stages in LDS; the host
+// uses the separate combine kernel beyond it.
+constexpr int kFusedMaxRowSplits = 4096;
+
+// Log-sum-exp combine of all splits for the R valid rows of one (b, kv head,
+// 32-row block), by one workgroup (gqa_split.py:134-147), spread over all 256
+// threads so the tail it adds stays short:
+//   1. m and l of every (row, split) into LDS; per-row m*; a = exp2(m - m*);
+//      l* = sum a * l;
+//   2. work items (split group, row, 4 columns): each sums a * acc over its
+//      splits; the split groups are then added up in LDS and o = sum / l*.
+// scratch: >= 2*R*S + 2*32 floats plus 1024 f32x4 (reuses the tile buffer).
 template <int DT, int D>
-__global__ __launch_bounds__(256) void gqa_split_first_kernel(SplitParams p) {
+__device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb, int t, float* scratch) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  constexpr int NDP = D / 4;
+  const Dims& dm = p.dm;
+  const int S = p.splits;
+  const int r0 = 32 * rb;
+  const int R = min(32, dm.G * dm.Sq - r0);  // valid rows: position-major packing
+  float* ma = scratch;              // [R][S]: m, then the scale factors a
+  float* la = ma + R * S;           // [R][S]: l
+  float* mst = la + R * S;          // [32]: m* per row
+  float* lst = mst + 32;            // [32]: l* per row
+  f32x4* red = reinterpret_cast<f32x4*>(scratch + ((2 * R * S + 64 + 3) & ~3));  // [NSG][R][NDP]
+
+  auto row_index = [&](int rl) {    // (b, head, pos) -> index of split 0 in the workspace
+    const int r = r0 + rl;
+    const int pos = r / dm.G, g = r - pos * dm.G;
+    return ((((int64_t)b * dm.Hq + kvh * dm.G + g) * dm.Sq + pos) * S);
+  };
+
+  for (int f = t; f < R * S; f += 256) {
+    const int rl = f / S, sp = f - rl * S;
+    const int64_t ix = row_index(rl) + sp;
+    ma[f] = load_coherent(p.ws_m + ix);
+    la[f] = load_coherent(p.ws_l + ix);
+  }
+  __syncthreads();
+  if (t < R) {
+    float m = -__builtin_inff();
+    for (int sp = 0; sp < S; ++sp) m = fmaxf(m, ma[t * S + sp]);
+    mst[t] = m;
+  }
+  __syncthreads();
+  // exp2(-inf - -inf) = NaN when every chunk of a row is empty, as the
+  // reference's combine (gqa_split.py:138) gives.
+  for (int f = t; f < R * S; f += 256) ma[f] = fast_exp2(ma[f] - mst[f / S]);
+  __syncthreads();
+  if (t < R) {
+    float l = 0.f;
+    for (int sp = 0; sp < S; ++sp) l += ma[t * S + sp] * la[t * S + sp];
+    lst[t] = l;
+  }
+
+  // Split groups: enough work items (<= 1024) to keep many loads in flight.
+  int nsg = 1024 / (R * NDP);
+  nsg = max(1, min(nsg, S));
+  const int items = nsg * R * NDP;
+  for (int it = t; it < items; it += 256) {
+    const int d4 = it % NDP;
+    const int rl = (it / NDP) % R;
+    const int sg = it / (NDP * R);
+    const float* wa = p.ws_acc + row_index(rl) * D + 4 * d4;
+    const float* a = ma + rl * S;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int sp = sg; sp < S; sp += nsg) {
+      const float* src = wa + (int64_t)sp * D;
+      const f32x4 x = {load_coherent(src), load_coherent(src + 1), load_coherent(src + 2), load_coherent(src + 3)};
+      o += a[sp] * x;
+    }
+    red[it] = o;
+  }
+  __syncthreads();
+  for (int f = t; f < R * NDP; f += 256) {
+    const int d4 = f % NDP, rl = f / NDP;
+    f32x4 o = red[f];
+    for (int sg = 1; sg < nsg; ++sg) o += red[sg * R * NDP + f];
+    const float l = lst[rl];
+    const int r = r0 + rl;
+    const int pos = r / dm.G, g = r - pos * dm.G;
+    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb +
+              (int64_t)(kvh * dm.G + g) * p.o.sh + (int64_t)pos * p.o.ss + 4 * d4;
+    u32x2 x;
+    x[0] = E::pack2(o[0] / l, o[1] / l);
+    x[1] = E::pack2(o[2] / l, o[3] / l);
+    *reinterpret_cast<u32x2*>(orow) = x;
+  }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_split_first_kernel(SplitParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
   using ST = SubTile<D>;
-  // One 128-key tile = two 64-key sub-tiles; reused for the final merge.
-  __shared__ __attribute__((aligned(16))) char smem[2 * ST::kBytes];
+  // One 128-key tile = two 64-key sub-tiles; reused for the wave merge and
+  // the fused combine.
+  constexpr int kCombineBytes = 2 * kFusedMaxRowSplits * 4 + 64 * 4 + 16 + 1024 * 16;
+  constexpr int kSmemBytes = 2 * ST::kBytes > kCombineBytes ? 2 * ST::kBytes : kCombineBytes;
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
   __shared__ float m_s[128], l_s[128];
 
   const Dims& dm = p.dm;
@@ -85,8 +180,8 @@ __global__ __launch_bounds__(256) void gqa_split_first_kernel(SplitParams p) {
 
   SubTileRegs<D> R0, R1;
   if (ntiles > 0) {
-    load_subtile<D, T>(R0, kbase, vbase, p.k.ss, p.v.ss, c0, c1, t);
-    load_subtile<D, T>(R1, kbase, vbase, p.k.ss, p.v.ss, c0 + 64, c1, t);
+    load_subtile<D, T, true>(R0, kbase, vbase, p.k.ss, p.v.ss, c0, c1, t);
+    load_subtile<D, T, true>(R1, kbase, vbase, p.k.ss, p.v.ss, c0 + 64, c1, t);
   }
   const int sub = wave >> 1, mb = wave & 1;
   const char* mytile = smem + sub * ST::kBytes;
@@ -98,8 +193,8 @@ __global__ __launch_bounds__(256) void gqa_split_first_kernel(SplitParams p) {
     store_subtile<D>(smem + ST::kBytes, R1, t);
     __syncthreads();
     if (it + 1 < ntiles) {
-      load_subtile<D, T>(R0, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys, c1, t);
-      load_subtile<D, T>(R1, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys + 64, c1, t);
+      load_subtile<D, T, true>(R0, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys, c1, t);
+      load_subtile<D, T, true>(R1, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys + 64, c1, t);
     }
 
     const int kb0 = key0 + 32 * wave;  // this wave's 32 keys
@@ -181,16 +276,38 @@ __global__ __launch_bounds__(256) void gqa_split_first_kernel(SplitParams p) {
       for (int j = 0; j < 4; ++j) o[j] += f * a_s[((ww * (D / 32) + db) * 4 + j) * 64 + lane];
     }
     if (valid) {
+      // Device-coherent stores: the fused combine may read them from another
+      // XCD within this launch.
       const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
       float* wa = p.ws_acc + row * D;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(wa + 32 * db + 8 * j + 4 * hh) = o[j];
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store_coherent(wa + 32 * db + 8 * j + 4 * hh + e, o[j][e]);
       if (db == 0 && hh == 0) {
-        p.ws_m[row] = mstar * c;
-        p.ws_l[row] = lsum;
+        store_coherent(p.ws_m + row, mstar * c);
+        store_coherent(p.ws_l + row, lsum);
       }
     }
   }
+
+  if (p.counters == nullptr) return;
+  // Fused combine: count this partial once its stores have completed, and let
+  // the workgroup that completes the count for this (b, kv head, row block)
+  // combine all splits.
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are done
+  __syncthreads();
+  if (t == 0) {
+    const int idx = (b * dm.Hkv + kvh) * p.n_rblk + rb;
+    const int prev = __hip_atomic_fetch_add(&p.counters[idx], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == p.splits - 1);
+    // Every increment of this call has landed: leave the counter zero.
+    if (s_last) __hip_atomic_store(&p.counters[idx], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  combine_rows<DT, D>(p, b, kvh, rb, t, reinterpret_cast<float*>(smem));
 }
 
 // LSE combine.  256 threads: thread (d4, sg) owns output columns
@@ -201,7 +318,7 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   using T = typename E::T;
   constexpr int ND4 = D / 4;
   constexpr int NSG = 256 / ND4;
-  __shared__ float red_m[256];
+  __shared__ float red_m[4];
   __shared__ f32x4 red_o[NSG][ND4];
   __shared__ float red_l[NSG][ND4];
 
@@ -212,19 +329,22 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   const float* wl = p.ws_l + (int64_t)row * S;
   const float* wa = p.ws_acc + (int64_t)row * S * D;
 
+  // m* = max over splits: per-thread max, wave max, then the 4 waves in LDS.
   float mx = -__builtin_inff();
+#pragma unroll 4
   for (int s = t; s < S; s += 256) mx = fmaxf(mx, wm[s]);
-  red_m[t] = mx;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((t & 63) == 0) red_m[t >> 6] = mx;
   __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) red_m[t] = fmaxf(red_m[t], red_m[t + off]);
-    __syncthreads();
-  }
-  const float mstar = red_m[0];
+  const float mstar = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
 
+  // Thread (d4, sg) sums its splits sg, sg + NSG, ...; unrolled so that the
+  // loads of several splits are in flight together.
   const int d4 = t % ND4, sg = t / ND4;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
+#pragma unroll 8
   for (int s = sg; s < S; s += NSG) {
     // exp2(-inf - -inf) = NaN when every chunk is empty, as gqa_split.py:138.
     const float a = fast_exp2(wm[s] - mstar);

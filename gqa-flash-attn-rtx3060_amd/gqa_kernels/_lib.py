@@ -39,6 +39,12 @@ SIGNATURES = {
         [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
     ),
     "gqa_split_reduce_launch": (_i, [_p, _i, _p, _i64x4, _i, _i, _i, _i, _i, _p]),
+    "gqa_split_counters_count": (ctypes.c_size_t, [_i, _i, _i, _i]),
+    "gqa_split_fused_launch": (
+        _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _p, _i,
+         _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
 }
 
 _lock = threading.Lock()

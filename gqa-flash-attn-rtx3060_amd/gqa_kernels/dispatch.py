@@ -31,8 +31,9 @@ SPLIT_MIN_KV = 1024
 # Keys per split-KV tile; a chunk is never shorter than this many tiles.
 SPLIT_TILE = 128
 SPLIT_MIN_TILES = 2
-# Target workgroups per compute unit for the split-KV first pass.
-SPLIT_WG_PER_CU = 4
+# Target workgroups per compute unit for the split-KV first pass (the kernel
+# runs two per CU at once; one round of workgroups measured fastest).
+SPLIT_WG_PER_CU = 2
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 

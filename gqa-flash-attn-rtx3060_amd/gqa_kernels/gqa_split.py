@@ -1,14 +1,16 @@
 """Split-KV forward for short query blocks against a long KV cache.
 
-Host side of the two-pass flash-decoding path (reference
-gqa_kernels/gqa_split.py:153-194): the fp32 partials live in one workspace
-allocated here with torch (caller-owned memory: the HIP library never
-allocates), then two C-ABI launches run the first pass and the log-sum-exp
-combine on torch's current stream.
+Host side of the flash-decoding path (reference gqa_kernels/gqa_split.py:153-194):
+the fp32 partials live in one workspace allocated here with torch
+(caller-owned memory: the HIP library never allocates).  By default two C-ABI
+launches run the first pass and then the log-sum-exp combine, the reference's
+structure; ``fused=True`` runs a single launch in which the last workgroup of
+each kv head combines.
 """
 from __future__ import annotations
 
 import math
+import threading
 
 import torch
 
@@ -16,7 +18,26 @@ from . import _lib
 
 __all__ = ["split_kv_forward", "workspace_bytes"]
 
+# Zeroed int32 counters for the fused combine, one buffer per (device,
+# stream): the kernel leaves them zero, so a buffer is reused by every call on
+# its stream (calls on one stream never overlap).
+_counters: dict = {}
+_counters_lock = threading.Lock()
+
+
+def _counter_buffer(device: torch.device, stream: int, n: int) -> torch.Tensor:
+    key = (device.index, stream)
+    with _counters_lock:
+        buf = _counters.get(key)
+        if buf is None or buf.numel() < n:
+            buf = torch.zeros(max(n, 1024), dtype=torch.int32, device=device)
+            _counters[key] = buf
+        return buf
+
 LOG2E = math.log2(math.e)
+# The fused combine stages (valid rows of a 32-row block) x splits values in
+# LDS; above this bound the two-launch form is used.
+FUSED_MAX_ROW_SPLITS = 4096
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 
@@ -26,8 +47,11 @@ def workspace_bytes(batch: int, num_heads: int, seq_q: int, head_dim: int, split
     return batch * num_heads * seq_q * splits * (head_dim + 2) * 4
 
 
-def split_kv_forward(q, k, v, causal, splits, workspace=None):
-    """Two-pass split-KV forward (first pass + LSE combine).
+def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False):
+    """Split-KV forward: first pass over `splits` chunks of the keys, then the
+    log-sum-exp combine (a second launch, or fused into the first pass with
+    ``fused=True``; the two-launch form measured faster on MI355X because the
+    fused combine of the last workgroup sits on the critical path).
 
     ``workspace`` may be a caller-provided fp32 CUDA tensor with at least
     ``workspace_bytes(...) / 4`` elements; otherwise one is allocated.
@@ -48,6 +72,22 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None):
     o = torch.empty_like(q)
 
     stream = torch.cuda.current_stream(q.device).cuda_stream
+    group = num_heads // num_kv_heads
+    if fused and min(32, group * seq_q) * splits <= FUSED_MAX_ROW_SPLITS:
+        n = lib.gqa_split_counters_count(batch, num_heads, num_kv_heads, seq_q)
+        counters = _counter_buffer(q.device, stream, n)
+        _lib.check(
+            lib.gqa_split_fused_launch(
+                q.data_ptr(), _lib.strides(q),
+                k.data_ptr(), _lib.strides(k),
+                v.data_ptr(), _lib.strides(v),
+                o.data_ptr(), _lib.strides(o),
+                workspace.data_ptr(), counters.data_ptr(), splits,
+                batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
+                scale_log2, int(bool(causal)), dtype, stream,
+            )
+        )
+        return o
     _lib.check(
         lib.gqa_split_first_launch(
             q.data_ptr(), _lib.strides(q),

@@ -98,6 +98,29 @@ int gqa_split_reduce_launch(const float* workspace, int splits,
                             int batch, int num_heads, int seq_q, int head_dim,
                             int dtype, void* stream);
 
+/* Number of int32 counters gqa_split_fused_launch needs: one per
+ * (batch, kv head, block of 32 packed (position, head) rows). */
+size_t gqa_split_counters_count(int batch, int num_heads, int num_kv_heads, int seq_q);
+
+/* Split-KV first pass with the log-sum-exp combine fused in: the last
+ * workgroup to finish each (batch, kv head, row block) combines the splits of
+ * its rows into o (same arithmetic as gqa_split_reduce_launch).  Together the
+ * two launches of reference gqa_kernels/gqa_split.py:168-193 in one kernel.
+ * counters (gqa_split_counters_count ints) must be zero on entry; the kernel
+ * leaves them zero, so one counter buffer can serve every call made on one
+ * stream (calls that overlap in time need separate buffers).  The combine
+ * stages min(32, G*seq_q) * splits values in LDS: above 4096 this returns
+ * GQA_E_SPLITS (use gqa_split_first_launch + gqa_split_reduce_launch). */
+int gqa_split_fused_launch(const void* q, const int64_t q_stride[4],
+                           const void* k, const int64_t k_stride[4],
+                           const void* v, const int64_t v_stride[4],
+                           void* o, const int64_t o_stride[4],
+                           float* workspace, int* counters, int splits,
+                           int batch, int num_heads, int num_kv_heads,
+                           int seq_q, int seq_kv, int head_dim,
+                           float scale_log2, int causal, int dtype,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -117,7 +117,7 @@ def test_baseline_70b_shape():
     k = torch.randn(B, Hkv, Skv, D, device=DEV, generator=g).to(torch.bfloat16)
     v = torch.randn(B, Hkv, Skv, D, device=DEV, generator=g).to(torch.bfloat16)
     r = _route(q, k)
-    assert r.kind == "split" and r.workgroups >= 1024, r
+    assert r.kind == "split" and r.workgroups >= 512, r
     out = _run(q, k, v)
     for b in (0, 7, 15):  # oracle on a deterministic subset of batch entries
         sl = slice(b, b + 1)
@@ -208,6 +208,38 @@ def test_split_partials_match_oracle(sq, skv, causal):
     norm = acc[full] / l[full][:, None]
     norm_o = acc_o[full] / l_o[full][:, None]
     assert np.abs(norm - norm_o).max() < 1e-2
+
+
+def test_fused_combine_matches_two_launch_path():
+    from gqa_kernels import gqa_split
+    for (B, Hq, Hkv, sq, skv, S) in ((1, 32, 8, 1, 4096, 16), (2, 64, 8, 4, 3001, 7), (1, 32, 8, 16, 2048, 64),
+                                     (1, 8, 2, 40, 200, 8)):
+        q, k, v = make_inputs(B, Hq, Hkv, sq, skv, 128, device=DEV, seed=S)
+        a = gqa_split.split_kv_forward(q, k, v, True, S, fused=True)
+        b = gqa_split.split_kv_forward(q, k, v, True, S, fused=False)
+        torch.cuda.synchronize()
+        # same partials, same combine arithmetic: equal up to summation order
+        mx, _ = errors(a, b)
+        assert mx <= 1.6e-2, (B, Hq, sq, skv, S, mx)
+        nan_a, nan_b = torch.isnan(a), torch.isnan(b)
+        assert torch.equal(nan_a, nan_b)
+        ref = oracle(q, k, v)
+        fin = ~np.isnan(ref)
+        assert_close(to_np(a)[fin], ref[fin], BASELINE_TOL[torch.bfloat16], "fused")
+    # the counters are left zero for the next call on this stream
+    for buf in gqa_split._counters.values():
+        assert int(buf.abs().sum().item()) == 0
+
+
+def test_fused_combine_repeated_calls():
+    from gqa_kernels import gqa_split
+    q, k, v = make_inputs(1, 32, 8, 1, 8192, 128, device=DEV, seed=9)
+    ref = oracle(q, k, v)
+    outs = [gqa_split.split_kv_forward(q, k, v, True, S, fused=True) for S in (64, 64, 3, 128, 64)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert_close(o, ref, BASELINE_TOL[torch.bfloat16], "repeat")
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[4])
 
 
 def test_split_count_invariance():

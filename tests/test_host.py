@@ -101,6 +101,24 @@ def test_empty_launches_are_noops(lib):
                               1, 32, 8, 0, 16, 128, 0.1, 1, 0, None) == 0
 
 
+def test_fused_launch_validation(lib):
+    f = lib.gqa_split_fused_launch
+    args = lambda ws, cnt, splits: (_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, ws, cnt, splits,
+                                    1, 32, 8, 1, 4096, 128, 0.1, 1, 0, None)
+    assert f(*args(_FAKE, None, 8)) == -7
+    assert f(*args(None, _FAKE, 8)) == -7
+    assert f(*args(_FAKE, _FAKE, 0)) == -5
+    assert f(*args(_FAKE, ctypes.c_void_p((1 << 20) + 2), 8)) == -4
+    # the fused combine stages min(32, G*seq_q) * splits values: 16 rows x 512 > 4096
+    big = (_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, _FAKE, 512,
+           1, 32, 8, 4, 4096, 128, 0.1, 1, 0, None)
+    assert f(*big) == -5
+    assert lib.gqa_split_counters_count(1, 32, 8, 1) == 8
+    assert lib.gqa_split_counters_count(16, 64, 8, 4) == 128
+    assert lib.gqa_split_counters_count(2, 32, 8, 16) == 2 * 8 * 2
+    assert lib.gqa_split_counters_count(1, 30, 8, 1) == 0
+
+
 def test_split_launch_validation(lib):
     f = lib.gqa_split_first_launch
     assert f(_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, 0, 1, 32, 8, 1, 4096, 128, 0.1, 1, 0, None) == -5
@@ -124,15 +142,15 @@ def test_route_baseline_configs():
     # prefill: single pass, 128 packed rows (32 positions x 4 heads) per workgroup
     r = choose_route(1, 32, 8, 16384, 16384, cu)
     assert r.kind == "single" and r.workgroups == 512 * 8
-    # decode 131072: split to 4 workgroups per CU
+    # decode 131072: split to 2 workgroups per CU
     r = choose_route(1, 32, 8, 1, 131072, cu)
-    assert r.kind == "split" and r.splits == 128 and r.workgroups == 1024
+    assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
     # decode 8192: limited by the minimum chunk (256 keys)
     r = choose_route(1, 32, 8, 1, 8192, cu)
     assert r.kind == "split" and r.splits == 32
     # 70B multi-token decode: 32 packed rows per kv head, 128 (b, kv head) pairs
     r = choose_route(16, 64, 8, 4, 32768, cu)
-    assert r.kind == "split" and r.splits == 8 and r.workgroups == 1024
+    assert r.kind == "split" and r.splits == 4 and r.workgroups == 512
     # chunked prefill: single pass
     assert choose_route(4, 32, 8, 512, 8192, cu).kind == "single"
     # reference decode cases below the split threshold stay single-pass
@@ -148,8 +166,9 @@ def test_route_properties():
                 assert r.kind == "split"
                 assert r.splits & (r.splits - 1) == 0  # power of two
                 assert r.splits == 1 or -(-skv // r.splits) >= SPLIT_MIN_TILES * SPLIT_TILE
-                # never more splits than needed for 4 workgroups per CU
-                assert r.splits == 1 or (r.workgroups // 2) < 4 * cu
+                # never more splits than needed for the per-CU target
+                from gqa_kernels.dispatch import SPLIT_WG_PER_CU
+                assert r.splits == 1 or (r.workgroups // 2) < SPLIT_WG_PER_CU * cu
 
 
 # ---------------------------------------------------------------------------
