@@ -286,26 +286,26 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 
 // Issue the direct-to-LDS loads (buffer_load_dwordx4 ... lds) of K rows
 // [key0, key0 + 64) into the K part of an FwdTile; the destination is
-// wave-uniform and each instruction covers 64 chunks.  Rows at or beyond
-// nrows_valid are not loaded (their LDS content is stale and every key there
-// is masked before use).  rk: descriptor of this (b, kv head)'s K rows;
+// wave-uniform and each instruction covers 64 chunks.  The loads are not
+// predicated: rk's extent ends at the last K row of this (b, kv head), so the
+// rows of a partial last tile beyond it read as zero (buffer range check) and
+// every key there is masked before use.  Straight-line issue keeps the key
+// loop free of branches, which also lets the compiler's wait-count analysis
+// see that the loads of the next tile never feed the current one.
 // k0b = key0 * key stride in bytes; koff: this lane's byte offset (its row in
 // the instruction times the key stride + its swizzled chunk).
 template <int D>
 __device__ inline void issue_k_dma(char* __restrict__ lds_tile, __amdgpu_buffer_rsrc_t rk, uint32_t k0b,
-                                   uint32_t kssb, uint32_t koff, int lane_row0, int nrows_valid, int wave) {
+                                   uint32_t kssb, uint32_t koff, int wave) {
   using FT = FwdTile<D>;
   constexpr int RPI = 64 / FT::CPR;                // rows per instruction
   constexpr int NI = (FT::kKeys * FT::CPR) / 256;  // instructions per thread
   typedef __attribute__((address_space(3))) void lds_void;
-  const bool full = nrows_valid >= FT::kKeys;
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int step = j * 4 + wave;  // instruction index within the tile
     lds_void* l = (lds_void*)(lds_tile + step * 1024);
-    const uint32_t so = k0b + (uint32_t)(step * RPI) * kssb;
-    if (full || lane_row0 + step * RPI < nrows_valid)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, l, 16, koff, so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, l, 16, koff, k0b + (uint32_t)(step * RPI) * kssb, 0, 0);
   }
 }
 
@@ -316,23 +316,14 @@ template <int D> struct VRegs {
   u32x2 v[KPT];
 };
 
-// rv: descriptor of this (b, kv head)'s V rows; k0b = key0 * key stride in
-// bytes; voff = kg*KPT*vssb + 8*d4; rows >= nrows_valid read as 0.
+// rv: descriptor of this (b, kv head)'s V rows, its extent ending at the last
+// row (rows beyond it read as 0); k0b = key0 * key stride in bytes;
+// voff = kg*KPT*vssb + 8*d4.
 template <int D>
 __device__ inline void load_v_regs(VRegs<D>& R, __amdgpu_buffer_rsrc_t rv, uint32_t k0b, uint32_t vssb,
-                                   uint32_t voff, int row0, int nrows_valid) {
-  constexpr int KPT = VRegs<D>::KPT;
-  if (nrows_valid >= 64) {
+                                   uint32_t voff) {
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) R.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, k0b + j * vssb, 0);
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    u32x2 x = {0u, 0u};
-    if (row0 + j < nrows_valid) x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, k0b + j * vssb, 0);
-    R.v[j] = x;
-  }
+  for (int j = 0; j < VRegs<D>::KPT; ++j) R.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, k0b + j * vssb, 0);
 }
 
 template <int D>
@@ -359,27 +350,32 @@ __device__ inline void store_v_lds(char* __restrict__ lds_tile, const VRegs<D>& 
 }
 
 // ---------------------------------------------------------------------------
-// Online softmax over one 32-key S^T block (16 values per lane; the two lane
-// halves hold the other 16 keys of the same row), exp2 domain.
+// Online softmax over one 64-key S^T tile held as two 32-key blocks (16
+// values per lane and block; the two lane halves hold the other 16 keys of
+// the same row), exp2 domain.  Split in two steps so the caller can run the
+// P*V product of the first block while the second is exponentiated.
 //
 // Lazy rescaling: the reference point m_ref of a row is only raised when the
-// block's max exceeds it by more than kRescaleLog2 (log2 units); otherwise the
+// tile's max exceeds it by more than kRescaleLog2 (log2 units); otherwise the
 // probabilities are computed against the stale m_ref and may reach
 // 2^kRescaleLog2, which bf16/fp16 P and fp32 l/acc hold exactly as well.  The
 // decision is wave-uniform, so in steady state the O accumulators are not
 // touched by the VALU at all.  The result o = acc / l is unchanged (both are
 // relative to the same m_ref).  A row whose m_ref is still -inf uses 0 as the
-// reference, so a fully masked block contributes p = 0, never NaN.
+// reference, so a fully masked tile contributes p = 0, never NaN.
 // ---------------------------------------------------------------------------
 constexpr float kRescaleLog2 = 8.0f;
 
-template <int DT, int NACC>
-__device__ inline void softmax_block(f32x16& s, float& m_ref, float& l_run, f32x16 (&acc)[NACC],
-                                     float c, u32x4 (&pk)[2]) {
-  using E = Elem<DT>;
-  float mx = fmaxf(s[0], s[1]);
+// Step 1: tile row max, and the (rare) rescale of l and the accumulators.
+// Returns -m_ref * c, the offset of the exponent for step 2.
+template <int NACC>
+__device__ inline float softmax_rescale(const f32x16 (&s)[2], float& m_ref, float& l_run, f32x16 (&acc)[NACC],
+                                        float c) {
+  float mx = fmaxf(s[0][0], s[0][1]);
 #pragma unroll
-  for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[v]);
+  for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
   mx = xhalf_max(mx);
   const bool grow = (mx - m_ref) * c > kRescaleLog2;  // false for NaN (both -inf)
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -393,8 +389,14 @@ __device__ inline void softmax_block(f32x16& s, float& m_ref, float& l_run, f32x
       for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
     m_ref = m_new;
   }
-  const float m_use = (m_ref == -__builtin_inff()) ? 0.f : m_ref;
-  const float nmc = -m_use * c;
+  return -((m_ref == -__builtin_inff()) ? 0.f : m_ref) * c;
+}
+
+// Step 2, per 32-key block: p = 2^(s*c - m_ref*c) in fp32, summed into l_run
+// in fp32, then rounded to the input type and packed as the P^T operand.
+template <int DT>
+__device__ inline void softmax_exp(const f32x16& s, float nmc, float& l_run, float c, u32x4 (&pk)[2]) {
+  using E = Elem<DT>;
   float pv[16];
   float rs = 0.f;
 #pragma unroll

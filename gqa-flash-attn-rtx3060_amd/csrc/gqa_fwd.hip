@@ -9,7 +9,8 @@
 //   online softmax     (exp2 domain, scale applied in fp32, gqa_fwd.py:98-101)
 //   O^T += V^T P^T     (P rounded to the input type, gqa_fwd.py:103)
 // K/V tiles are double-buffered in LDS; the next tile's global loads are in
-// flight while the current one is computed.  Causal: the key loop stops at
+// flight while the current one is computed (K straight into LDS by buffer
+// loads with the LDS-DMA form, V through registers and a transposing store).  Causal: the key loop stops at
 // the workgroup's last visible key (gqa_fwd.py:70-73) and masks only the
 // tiles that cross the diagonal or the end of the keys.
 #include <type_traits>
@@ -76,13 +77,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ntiles = (kv_end + FT::kKeys - 1) / FT::kKeys;
   const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
 
-  // Global side: buffer descriptors over this (b, kv head)'s K and V rows
-  // (the host guarantees seq_kv * key stride * 2 < 2^31), per-lane offsets.
+  // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
+  // each ending at the last byte of row seq_kv - 1 so that rows past the end
+  // read as zero (the host guarantees seq_kv * key stride * 2 < 2^31), and
+  // per-lane offsets.
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
   const char* kbh = static_cast<const char*>(p.k.ptr) + 2 * ((int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh);
   const char* vbh = static_cast<const char*>(p.v.ptr) + 2 * ((int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbh, 0x7fffffffu);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, 0x7fffffffu);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbh, (uint32_t)(dm.Skv - 1) * kssb + 2 * D);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, (uint32_t)(dm.Skv - 1) * vssb + 2 * D);
   const int lrow = lane / CPR;
   const uint32_t koff =
       (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ FT::gk((wave * RPI + lrow) & 15));
@@ -119,9 +122,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   VRegs<D> R;
   if (ntiles > 0) {
-    const int nv = min(FT::kKeys, dm.Skv);
-    issue_k_dma<D>(smem0, rk, 0u, kssb, koff, lrow, nv, wave);
-    load_v_regs<D>(R, rv, 0u, vssb, voff, kg * KPT, nv);
+    issue_k_dma<D>(smem0, rk, 0u, kssb, koff, wave);
+    load_v_regs<D>(R, rv, 0u, vssb, voff);
     store_v_lds<D>(smem0, R, t);
   }
   __syncthreads();
@@ -133,39 +135,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int key0 = it * FT::kKeys;
     const bool has_next = it + 1 < ntiles;
     if (has_next) {
-      const int k1 = key0 + FT::kKeys;
-      const int nv = min(FT::kKeys, dm.Skv - k1);
-      issue_k_dma<D>(nxt, rk, (uint32_t)k1 * kssb, kssb, koff, lrow, nv, wave);
-      load_v_regs<D>(R, rv, (uint32_t)k1 * vssb, vssb, voff, kg * KPT, nv);
+      const uint32_t k1 = (uint32_t)(key0 + FT::kKeys);
+      issue_k_dma<D>(nxt, rk, k1 * kssb, kssb, koff, wave);
+      load_v_regs<D>(R, rv, k1 * vssb, vssb, voff);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // S^T = K Q^T for the two 32-key blocks, the chains interleaved and each
+    // K operand read from LDS four MFMAs ahead of its use.
+    f32x16 sc[2];
+    sc[0] = f32x16{};
+    sc[1] = f32x16{};
+    {
+      u32x4 ak[D / 16][2];
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+          ak[ks][mb] = *reinterpret_cast<const u32x4*>(cur + mb * 32 * (2 * D) + ka[ks]);
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) sc[mb] = E::mfma(ak[ks][mb], qreg[ks], sc[mb]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 LDS reads
+#pragma unroll
+      for (int j = 0; j < D / 8 - 4; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // last 4 MFMAs
     }
 
     const bool need_mask = (key0 + FT::kKeys > dm.Skv) || (dm.causal && key0 + FT::kKeys - 1 > qpos_lo);
-    // Issue both S^T chains first: block 1's MFMAs then execute while the
-    // softmax of block 0 runs on the VALU, and PV of block 0 overlaps the
-    // softmax of block 1.
-    f32x16 sc[2];
+    if (need_mask) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      sc[mb] = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(cur + mb * 32 * (2 * D) + ka[ks]);
-        sc[mb] = E::mfma(a, qreg[ks], sc[mb]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      if (need_mask) {
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = key0 + 32 * mb + key_of(v, hh);
           const bool off = key >= dm.Skv || (dm.causal && key > qpos);
           sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
-      }
+    }
+    const float nmc = softmax_rescale<D / 32>(sc, m_run, l_run, acc, c);
+    // P of block 0 feeds its PV MFMAs while block 1 is exponentiated.
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
       u32x4 pk[2];
-      softmax_block<DT, D / 32>(sc[mb], m_run, l_run, acc, c, pk);
+      softmax_exp<DT>(sc[mb], nmc, l_run, c, pk);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -173,7 +190,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const u32x4 a = *reinterpret_cast<const u32x4*>(cur + 4096 * db + va[mb ^ (db & 1)][kk]);
           acc[db] = E::mfma(a, pk[kk], acc[db]);
         }
-      if (mb == 0) __builtin_amdgcn_sched_barrier(0);
     }
 
     if (has_next) store_v_lds<D>(nxt, R, t);
