@@ -37,6 +37,12 @@ int check_tensor(const void* ptr, const int64_t st[4]) {
   return GQA_OK;
 }
 
+// The single-pass kernel addresses one (batch, kv head)'s K or V rows with
+// 32-bit byte offsets, up to two 64-key tiles past the last row.
+bool rows_fit_32bit(int seq_kv, const int64_t st[4]) {
+  return ((int64_t)seq_kv + 192) * st[2] * 2 < ((int64_t)1 << 31);
+}
+
 TensorRef ref(const void* ptr, const int64_t st[4]) { return TensorRef{ptr, st[0], st[1], st[2]}; }
 
 int to_code(hipError_t e) { return e == hipSuccess ? GQA_OK : static_cast<int>(e); }
@@ -53,9 +59,11 @@ const char* gqa_strerror(int code) {
     case GQA_E_SHAPE: return "invalid shape: sizes must be non-negative and num_heads divisible by num_kv_heads";
     case GQA_E_HEAD_DIM: return "unsupported head_dim (supported: 64, 128)";
     case GQA_E_DTYPE: return "unsupported dtype (supported: bf16, fp16)";
-    case GQA_E_STRIDE: return "unsupported layout: last dim must be contiguous and rows 16-byte aligned";
+    case GQA_E_STRIDE:
+      return "unsupported layout: last dim must be contiguous, rows 16-byte aligned, and one head's K/V rows "
+             "within 2 GiB";
     case GQA_E_SPLITS: return "splits out of range [1, GQA_MAX_SPLITS]";
-    case GQA_E_GROUP: return "group size (num_heads / num_kv_heads) larger than 128";
+    case GQA_E_GROUP: return "group size (num_heads / num_kv_heads) larger than 256";
     case GQA_E_NULL: return "null pointer argument";
     default: break;
   }
@@ -87,6 +95,7 @@ int gqa_fwd_launch(const void* q, const int64_t q_stride[4], const void* k, cons
   if (batch == 0 || seq_q == 0) return GQA_OK;
   if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
   if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
+  if (seq_kv > 0 && (!rows_fit_32bit(seq_kv, k_stride) || !rows_fit_32bit(seq_kv, v_stride))) return GQA_E_STRIDE;
 
   gqa::FwdParams p;
   p.q = ref(q, q_stride);

@@ -249,166 +249,10 @@ __device__ inline void pv_block(const char* __restrict__ lds, const u32x4 p[2], 
   }
 }
 
-// ---------------------------------------------------------------------------
-// Single-pass LDS tile (64 keys x D), double-buffered.
-//
-// K part: row-major, 16-byte chunks, chunk cd of row r stored at cd ^ gk(r).
-// K is written by direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes
-// write 1 KiB contiguous), so the swizzle is applied on the global side: the
-// lane that lands on physical chunk pc of row r fetches chunk pc ^ gk(r).
-// gk is chosen so that the S^T A-operand reads (row pi(i), chunk 2ks+h) hit
-// 16 distinct 16-byte bank groups in every 16 consecutive lanes and 8 distinct
-// groups modulo 128 bytes in every 8 lanes (conflict-free whether the LDS
-// serves 8 or 16 lanes of a 128-bit read per cycle).  With that gk,
-// gk(pi(i)) = i & (CPR - 1): the read chunk of lane i is simply (2ks+h) ^ i.
-//
-// V part: transposed [d][key], chunks of 8 keys, chunk c of row d stored at
-// c ^ f(d), f(d) = (d + d/8) & 7 (the same layout as SubTile).
-// ---------------------------------------------------------------------------
-template <int D> struct FwdTile {
-  static constexpr int kKeys = 64;
-  static constexpr int CPR = D / 8;  // 16-byte chunks per K row
-  static constexpr int kKBytes = kKeys * D * 2;
-  static constexpr int kVBytes = D * kKeys * 2;
-  static constexpr int kBytes = kKBytes + kVBytes;
-
-  __device__ static constexpr int gk(int r) {
-    return CPR == 16 ? ((r & 3) | (((r >> 3) & 1) << 2) | (((r >> 2) & 1) << 3))
-                     : ((r & 3) | (((r >> 3) & 1) << 2));
-  }
-  __device__ static constexpr int f0(int i) { return (i + (i >> 3)) & 7; }
-};
-
-// Buffer resource over `bytes` bytes at `base` (raw buffer, stride 0).
+// Buffer resource over `bytes` bytes at `base` (raw buffer, stride 0): loads
+// at offsets at or beyond `bytes` return zero instead of touching memory.
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-
-// Issue the direct-to-LDS loads (buffer_load_dwordx4 ... lds) of K rows
-// [key0, key0 + 64) into the K part of an FwdTile; the destination is
-// wave-uniform and each instruction covers 64 chunks.  The loads are not
-// predicated: rk's extent ends at the last K row of this (b, kv head), so the
-// rows of a partial last tile beyond it read as zero (buffer range check) and
-// every key there is masked before use.  Straight-line issue keeps the key
-// loop free of branches, which also lets the compiler's wait-count analysis
-// see that the loads of the next tile never feed the current one.
-// k0b = key0 * key stride in bytes; koff: this lane's byte offset (its row in
-// the instruction times the key stride + its swizzled chunk).
-template <int D>
-__device__ inline void issue_k_dma(char* __restrict__ lds_tile, __amdgpu_buffer_rsrc_t rk, uint32_t k0b,
-                                   uint32_t kssb, uint32_t koff, int wave) {
-  using FT = FwdTile<D>;
-  constexpr int RPI = 64 / FT::CPR;                // rows per instruction
-  constexpr int NI = (FT::kKeys * FT::CPR) / 256;  // instructions per thread
-  typedef __attribute__((address_space(3))) void lds_void;
-#pragma unroll
-  for (int j = 0; j < NI; ++j) {
-    const int step = j * 4 + wave;  // instruction index within the tile
-    lds_void* l = (lds_void*)(lds_tile + step * 1024);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, l, 16, koff, k0b + (uint32_t)(step * RPI) * kssb, 0, 0);
-  }
-}
-
-// V staging for one 64-key tile: thread owns keys [KPT*kg, KPT*kg + KPT) x
-// d [4*d4, 4*d4 + 4), d4 = t % (D/4), kg = t / (D/4), KPT = D/16.
-template <int D> struct VRegs {
-  static constexpr int KPT = D / 16;
-  u32x2 v[KPT];
-};
-
-// rv: descriptor of this (b, kv head)'s V rows, its extent ending at the last
-// row (rows beyond it read as 0); k0b = key0 * key stride in bytes;
-// voff = kg*KPT*vssb + 8*d4.
-template <int D>
-__device__ inline void load_v_regs(VRegs<D>& R, __amdgpu_buffer_rsrc_t rv, uint32_t k0b, uint32_t vssb,
-                                   uint32_t voff) {
-#pragma unroll
-  for (int j = 0; j < VRegs<D>::KPT; ++j) R.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, k0b + j * vssb, 0);
-}
-
-template <int D>
-__device__ inline void store_v_lds(char* __restrict__ lds_tile, const VRegs<D>& R, int t) {
-  using FT = FwdTile<D>;
-  constexpr int KPT = VRegs<D>::KPT;
-  const int d4 = t % (D / 4), kg = t / (D / 4);
-#pragma unroll
-  for (int dd = 0; dd < 4; ++dd) {
-    const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-    uint32_t w[KPT / 2];
-#pragma unroll
-    for (int i = 0; i < KPT / 2; ++i) w[i] = __builtin_amdgcn_perm(R.v[2 * i + 1][dd >> 1], R.v[2 * i][dd >> 1], sel);
-    const int d = 4 * d4 + dd;
-    const int f = (d + (d >> 3)) & 7;
-    if constexpr (KPT == 8) {
-      u32x4 o = {w[0], w[1], w[2], w[3]};
-      *reinterpret_cast<u32x4*>(lds_tile + FT::kKBytes + d * 128 + ((kg ^ f) << 4)) = o;
-    } else {
-      u32x2 o = {w[0], w[1]};
-      *reinterpret_cast<u32x2*>(lds_tile + FT::kKBytes + d * 128 + (((kg >> 1) ^ f) << 4) + ((kg & 1) << 3)) = o;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Online softmax over one 64-key S^T tile held as two 32-key blocks (16
-// values per lane and block; the two lane halves hold the other 16 keys of
-// the same row), exp2 domain.  Split in two steps so the caller can run the
-// P*V product of the first block while the second is exponentiated.
-//
-// Lazy rescaling: the reference point m_ref of a row is only raised when the
-// tile's max exceeds it by more than kRescaleLog2 (log2 units); otherwise the
-// probabilities are computed against the stale m_ref and may reach
-// 2^kRescaleLog2, which bf16/fp16 P and fp32 l/acc hold exactly as well.  The
-// decision is wave-uniform, so in steady state the O accumulators are not
-// touched by the VALU at all.  The result o = acc / l is unchanged (both are
-// relative to the same m_ref).  A row whose m_ref is still -inf uses 0 as the
-// reference, so a fully masked tile contributes p = 0, never NaN.
-// ---------------------------------------------------------------------------
-constexpr float kRescaleLog2 = 8.0f;
-
-// Step 1: tile row max, and the (rare) rescale of l and the accumulators.
-// Returns -m_ref * c, the offset of the exponent for step 2.
-template <int NACC>
-__device__ inline float softmax_rescale(const f32x16 (&s)[2], float& m_ref, float& l_run, f32x16 (&acc)[NACC],
-                                        float c) {
-  float mx = fmaxf(s[0][0], s[0][1]);
-#pragma unroll
-  for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
-#pragma unroll
-  for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
-  mx = xhalf_max(mx);
-  const bool grow = (mx - m_ref) * c > kRescaleLog2;  // false for NaN (both -inf)
-  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-    const float m_new = fmaxf(m_ref, mx);
-    const float m_new_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = fast_exp2((m_ref - m_new_use) * c);
-    l_run *= alpha;
-#pragma unroll
-    for (int db = 0; db < NACC; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
-    m_ref = m_new;
-  }
-  return -((m_ref == -__builtin_inff()) ? 0.f : m_ref) * c;
-}
-
-// Step 2, per 32-key block: p = 2^(s*c - m_ref*c) in fp32, summed into l_run
-// in fp32, then rounded to the input type and packed as the P^T operand.
-template <int DT>
-__device__ inline void softmax_exp(const f32x16& s, float nmc, float& l_run, float c, u32x4 (&pk)[2]) {
-  using E = Elem<DT>;
-  float pv[16];
-  float rs = 0.f;
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    pv[v] = fast_exp2(__builtin_fmaf(s[v], c, nmc));
-    rs += pv[v];
-  }
-  l_run += rs;
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pk[kk][e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,18 +1,38 @@
 // gqa_fwd.hip — single-pass group-packed GQA forward for gfx950.
 //
 // Replaces the Triton kernel gqa_fwd_kernel (reference
-// gqa_kernels/gqa_fwd.py:33-109).  One workgroup = 4 waves = 128 packed
-// query rows of ONE (batch, kv head): G query heads x block_m positions
-// (row r -> head r / block_m, position r % block_m, as gqa_fwd.py:58-63), so
-// each K/V tile staged in LDS feeds the whole query group.  Per 64-key tile:
+// gqa_kernels/gqa_fwd.py:33-109).  One workgroup = 8 waves = 256 packed query
+// rows of ONE (batch, kv head): G query heads x block_m positions (row r ->
+// head r / block_m, position r % block_m, as gqa_fwd.py:58-63), so each K/V
+// tile staged in LDS feeds the whole query group.  Per 64-key tile and wave
+// (32 rows):
 //   S^T = K Q^T        (bf16/f16 MFMA 32x32x16, fp32 accumulate)
 //   online softmax     (exp2 domain, scale applied in fp32, gqa_fwd.py:98-101)
 //   O^T += V^T P^T     (P rounded to the input type, gqa_fwd.py:103)
-// K/V tiles are double-buffered in LDS; the next tile's global loads are in
-// flight while the current one is computed (K straight into LDS by buffer
-// loads with the LDS-DMA form, V through registers and a transposing store).  Causal: the key loop stops at
-// the workgroup's last visible key (gqa_fwd.py:70-73) and masks only the
-// tiles that cross the diagonal or the end of the keys.
+// Causal: the key loop stops at the workgroup's last visible key
+// (gqa_fwd.py:70-73) and masks only the tiles that cross the diagonal or the
+// end of the keys.
+//
+// Schedule ("ping-pong").  The waves form two groups of four, A = waves 0-3
+// and B = waves 4-7; wave w and wave w+4 share a SIMD.  Work alternates
+// between MFMA phases (the P*V product of the previous tile and S^T of the
+// current one: 32 MFMAs per wave) and softmax phases (VALU only), and the two
+// groups run one phase apart, separated by workgroup barriers: while one
+// group's MFMAs occupy the matrix core of a SIMD, the other group's softmax
+// runs on the same SIMD's vector ALU.
+//
+//   phase:   0       1       2       3       4     ...
+//   A:     S(0)    sm(0)   PV(0)   sm(1)   PV(1)
+//                          +S(1)           +S(2)
+//   B:     (idle)  S(0)    sm(0)   PV(0)   sm(1)
+//                                  +S(1)
+//
+// K and V tiles are both loaded straight into LDS (buffer loads in their
+// LDS-DMA form) through a ring of three stages; stage t holds K(t) and
+// V(t-1), the operands of MFMA phase t.  Each softmax phase issues the loads
+// two tiles ahead (group A: K, group B: V) and waits for the ones issued one
+// softmax phase earlier, so a load has two phases to land and the ring never
+// overwrites a stage that is still read.
 #include <type_traits>
 
 #include "gqa_common.hpp"
@@ -20,23 +40,208 @@
 
 namespace gqa {
 
+// ---------------------------------------------------------------------------
+// One pipeline stage in LDS: a 64-key K tile and a 64-key V tile, both
+// row-major [key][d] in 16-byte chunks, written by direct-to-LDS loads
+// (64 lanes write 1 KiB contiguous per instruction), so both swizzles are
+// applied on the global side: the lane that lands on chunk pc of row r
+// fetches chunk pc ^ swizzle(r).
+//
+// K: gk is chosen so that the S^T A-operand reads (row pi(i), chunk 2ks+h)
+// hit distinct bank groups in every 16 consecutive lanes; with it,
+// gk(pi(i)) = i & (CPR - 1), so the chunk lane i reads is (2ks+h) ^ i.
+//
+// V: read transposed by ds_read_b64_tr_b16.  In each 16-lane group of such a
+// read, lane j addresses V[r0 + j/4][d0 + 4*(j%4)] and receives
+// V[r0 + k][d0 + j] for k = 0..3: 4 keys of one d, the layout of the V^T
+// A operand.  A group touches 4 rows x 32 bytes; sv moves the 4 rows to
+// distinct bank groups and keeps the two groups of a half-wave (d0 and
+// d0 + 16) apart, so the read is conflict-free.
+// ---------------------------------------------------------------------------
+template <int D> struct FwdStage {
+  static constexpr int kKeys = 64;
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int kTileBytes = kKeys * D * 2;  // one K or V tile
+  static constexpr int RPI = 64 / CPR;              // rows per LDS-DMA instruction
+  static constexpr int NI = (kKeys * CPR) / 256;    // LDS-DMA instructions per wave of a group
+
+  __device__ static constexpr int gk(int r) {
+    return CPR == 16 ? ((r & 3) | (((r >> 3) & 1) << 2) | (((r >> 2) & 1) << 3))
+                     : ((r & 3) | (((r >> 3) & 1) << 2));
+  }
+  __device__ static constexpr int sv(int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+};
+
+// Direct-to-LDS loads of tile rows [key0, key0 + 64) by the 4 waves of one
+// group (wave index gw): NI instructions each, 64 lanes x 16 bytes per
+// instruction.  Not predicated: the descriptor's extent ends at the last row
+// of this (b, kv head), so rows past it read as zero (and are masked, or
+// belong to a tile that is never used).  k0b = key0 * row stride in bytes;
+// off: this lane's row in the instruction times the row stride plus its
+// swizzled chunk.
+template <int D>
+__device__ inline void issue_tile_dma(char* __restrict__ lds, __amdgpu_buffer_rsrc_t rsrc, uint32_t k0b,
+                                      uint32_t rowb, uint32_t off, int gw) {
+  using ST = FwdStage<D>;
+  typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+  for (int j = 0; j < ST::NI; ++j) {
+    const int step = j * 4 + gw;  // instruction index within the tile
+    lds_void* l = (lds_void*)(lds + step * 1024);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, l, 16, off, k0b + (uint32_t)(step * ST::RPI) * rowb, 0, 0);
+  }
+}
+
+typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ inline u32x2 ld_tr(const char* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
+}
+
+// s_waitcnt immediates (gfx9 encoding): vmcnt(n) alone, and lgkmcnt(0) alone.
+__device__ constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+constexpr int kLgkm0 = 0xC07F;
+
+// Workgroup barrier between phases, without a memory fence: this wave's LDS
+// reads are complete (lgkmcnt(0)); completion of its LDS-DMA loads is waited
+// for explicitly, where the schedule needs it.  The empty asm statements keep
+// the compiler from moving memory accesses across the barrier.
+__device__ inline void phase_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(kLgkm0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+}
+
+// Keep a value computed in the current phase: without it the compiler may
+// sink the computation past the barrier, next to its use in the next phase,
+// which would move VALU work into an MFMA phase.
+template <typename V>
+__device__ inline void pin(V& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// v_max3_f32 without the canonicalising moves the compiler adds in front of
+// fmaxf on MFMA results (finite or -inf here; no NaN handling needed).
+__device__ inline float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Online softmax of one 64-key S^T tile held as two 32-key blocks (16 values
+// per lane and block; the two lane halves hold the other 16 keys of the
+// same row), exp2 domain.
+//
+// Lazy rescaling: the reference point m_ref of a row is only raised when the
+// tile's max exceeds it by more than kRescaleLog2 (log2 units); otherwise the
+// probabilities are computed against the stale m_ref and may reach
+// 2^kRescaleLog2, which bf16/fp16 P and fp32 l/acc hold exactly as well.  The
+// decision is wave-uniform, so in steady state the O accumulators are not
+// touched by the VALU at all.  The result o = acc / l is unchanged (both are
+// relative to the same m_ref).  A row whose m_ref is still -inf uses 0 as the
+// reference, so a fully masked tile contributes p = 0, never NaN.
+// ---------------------------------------------------------------------------
+constexpr float kRescaleLog2 = 8.0f;
+
+// Tile row max (a max3 tree), and the rare rescale of l and the
+// accumulators.  Returns -m_ref * c, the offset of the exponent.
+template <int NACC>
+__device__ inline float softmax_rescale(const f32x16 (&s)[2], float& m_ref, float& l_run, f32x16 (&acc)[NACC],
+                                        float c) {
+  float m1[11];
+#pragma unroll
+  for (int k = 0; k < 10; ++k) {
+    const int i0 = 3 * k, i1 = 3 * k + 1, i2 = 3 * k + 2;
+    m1[k] = vmax3(s[i0 >> 4][i0 & 15], s[i1 >> 4][i1 & 15], s[i2 >> 4][i2 & 15]);
+  }
+  m1[10] = vmax3(s[1][14], s[1][15], s[1][15]);
+  const float n0 = vmax3(m1[0], m1[1], m1[2]), n1 = vmax3(m1[3], m1[4], m1[5]);
+  const float n2 = vmax3(m1[6], m1[7], m1[8]), n3 = vmax3(m1[9], m1[10], m1[10]);
+  const float mx = xhalf_max(vmax3(vmax3(n0, n1, n2), n3, n3));
+  const bool grow = (mx - m_ref) * c > kRescaleLog2;  // false for NaN (both -inf)
+  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    const float m_new = fmaxf(m_ref, mx);
+    const float m_new_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = fast_exp2((m_ref - m_new_use) * c);
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < NACC; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
+    m_ref = m_new;
+  }
+  return -((m_ref == -__builtin_inff()) ? 0.f : m_ref) * c;
+}
+
+// One 32-key block: p = 2^(s*c - m_ref*c) in fp32, rounded to the input type
+// and packed as the P^T operand; returns the fp32 row sum (a tree).
+template <int DT>
+__device__ inline float softmax_exp(const f32x16& s, float nmc, float c, u32x4 (&pk)[2]) {
+  using E = Elem<DT>;
+  float pv[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) pv[v] = fast_exp2(__builtin_fmaf(s[v], c, nmc));
+  float s8[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s8[j] = pv[2 * j] + pv[2 * j + 1];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pk[kk][e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
+  return ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+}
+
+// ---------------------------------------------------------------------------
+// Instruction schedule of an MFMA phase: slot j is one MFMA; the LDS reads of
+// slot j + P are issued right after MFMA j (P slots ahead, to cover the LDS
+// latency).  Slots [0, NRD2) are P*V MFMAs with two transposing reads each,
+// the rest S^T MFMAs with one 16-byte read each.
+// ---------------------------------------------------------------------------
+template <int NRD2, int NSLOT, int P, int J>
+__device__ __forceinline__ void mphase_prefetch() {
+  if constexpr (J < P && J < NSLOT) {
+    __builtin_amdgcn_sched_group_barrier(0x100, (J < NRD2) ? 2 : 1, 0);  // LDS reads
+    mphase_prefetch<NRD2, NSLOT, P, J + 1>();
+  }
+}
+template <int NRD2, int NSLOT, int P, int J>
+__device__ __forceinline__ void mphase_pipe() {
+  if constexpr (J < NSLOT) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    if constexpr (J + P < NSLOT) __builtin_amdgcn_sched_group_barrier(0x100, (J + P < NRD2) ? 2 : 1, 0);
+    mphase_pipe<NRD2, NSLOT, P, J + 1>();
+  }
+}
+
 template <int DT, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
-  using FT = FwdTile<D>;
-  constexpr int CPR = FT::CPR;
-  constexpr int RPI = 64 / CPR;
-  constexpr int KPT = VRegs<D>::KPT;
-  // Two separate arrays (not one array of two halves): the compiler can then
-  // tell the DMA target of the next tile from the buffer being read, and does
-  // not wait for the in-flight loads before the reads of the current tile.
-  __shared__ __attribute__((aligned(1024))) char smem0[FT::kBytes];
-  __shared__ __attribute__((aligned(1024))) char smem1[FT::kBytes];
+  using ST = FwdStage<D>;
+  constexpr int CPR = ST::CPR;
+  constexpr int NDB = D / 32;  // 32-wide d blocks of O^T
+  constexpr int NKS = D / 16;  // k-steps of S^T
+  constexpr int PF = 6;        // MFMA slots of LDS-read lookahead
+  // Six separate arrays (not one): the compiler can then tell the LDS-DMA
+  // targets of later tiles from the buffers being read, and does not wait for
+  // those loads before the reads.
+  __shared__ __attribute__((aligned(1024))) char sk0[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sk1[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sk2[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sv0[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sv1[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sv2[ST::kTileBytes];
 
   const Dims& dm = p.dm;
   const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;  // wave-uniform (SGPR), 0..3
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 7;  // wave-uniform (SGPR)
+  const int grp = wave >> 2;                                     // 0: group A, 1: group B
+  const int gw = wave & 3;                                       // wave index in its group
   const int i = lane & 31, hh = lane >> 5;
 
   // Work item: heavy (late) query blocks first under causal, and every XCD
@@ -56,12 +261,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int head = kvh * dm.G + (g < dm.G ? g : 0);
   const int qpos = pos + (dm.Skv - dm.Sq);
 
-  u32x4 qreg[D / 16];
+  u32x4 qreg[NKS];
   {
     const T* qrow = static_cast<const T*>(p.q.ptr) + (int64_t)b * p.q.sb + (int64_t)head * p.q.sh +
                     (int64_t)(valid ? pos : 0) * p.q.ss;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
+    for (int ks = 0; ks < NKS; ++ks) {
       u32x4 x = {0u, 0u, 0u, 0u};
       if (valid) x = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
       qreg[ks] = x;
@@ -74,13 +279,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int kv_end = dm.Skv;
   if (dm.causal) kv_end = min(dm.Skv, pos_hi + (dm.Skv - dm.Sq) + 1);
   kv_end = max(kv_end, 0);
-  const int ntiles = (kv_end + FT::kKeys - 1) / FT::kKeys;
+  const int ntiles = (kv_end + ST::kKeys - 1) / ST::kKeys;
   const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
 
   // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
-  // each ending at the last byte of row seq_kv - 1 so that rows past the end
-  // read as zero (the host guarantees seq_kv * key stride * 2 < 2^31), and
-  // per-lane offsets.
+  // each ending at the last byte of row seq_kv - 1, and per-lane offsets.
+  // The host guarantees (seq_kv + 192) * row stride * 2 < 2^31, so every
+  // offset below (up to two tiles past the end) fits 32 bits.
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
   const char* kbh = static_cast<const char*>(p.k.ptr) + 2 * ((int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh);
   const char* vbh = static_cast<const char*>(p.v.ptr) + 2 * ((int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh);
@@ -88,85 +293,128 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, (uint32_t)(dm.Skv - 1) * vssb + 2 * D);
   const int lrow = lane / CPR;
   const uint32_t koff =
-      (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ FT::gk((wave * RPI + lrow) & 15));
-  const int d4 = t % (D / 4), kg = t / (D / 4);
-  const uint32_t voff = (uint32_t)(kg * KPT * vssb) + 8u * (uint32_t)d4;
+      (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ ST::gk((gw * ST::RPI + lrow) & 15));
+  const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ ST::sv(lrow));
 
-  // LDS side: per-lane read offsets (the tile buffer, the 32-key block and
-  // the 32-row d block are immediate offsets on top of these).  The masks are
-  // no-ops on the values; they give the compiler known bounds, so it can prove
-  // that reads of one buffer never touch the other and does not wait for the
-  // next tile's in-flight loads.
-  constexpr uint32_t kKMask = (FT::kKBytes / 2 - 1) & ~15u;  // rows 0..31 of K
-  constexpr uint32_t kVMask = (FT::kBytes - 1) & ~15u;
-  uint32_t ka[D / 16];
+  // LDS side: per-lane read offsets (the 32-key block, chunk and row offsets
+  // of each read are immediates on top of these).  The masks are no-ops on
+  // the values; they give the compiler known bounds.
+  constexpr uint32_t kKMask = (ST::kTileBytes / 2 - 1) & ~15u;
+  constexpr uint32_t kVMask = (ST::kTileBytes - 1) & ~7u;
+  uint32_t ka[NKS];
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks)
+  for (int ks = 0; ks < NKS; ++ks)
     ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
-  uint32_t va[2][2];
+  uint32_t vb[NDB];
   {
-    const int z = hh ^ FT::f0(i);
+    const int q = lane >> 4, ii = lane & 15;                  // 16-lane group, lane in group
+    const int rowl = 8 * (q >> 1) + (ii >> 2);                // key row addressed by this lane
+    const int f = (CPR == 16) ? (ii >> 2) : ((ii >> 3) & 1);  // sv(rowl) / 4
 #pragma unroll
-    for (int mp = 0; mp < 2; ++mp)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        va[mp][kk] = (uint32_t)(FT::kKBytes + 128 * i + 16 * ((4 * mp + 2 * kk) ^ z)) & kVMask;
+    for (int db = 0; db < NDB; ++db)
+      vb[db] = (uint32_t)(rowl * (2 * D) + 16 * (4 * (db ^ f) + 2 * (q & 1) + ((ii & 3) >> 1)) + 8 * (ii & 1)) &
+               kVMask;
   }
 
-  f32x16 acc[D / 32];
+  f32x16 acc[NDB];
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) acc[db] = f32x16{};
+  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
   float m_run = -__builtin_inff();
   float l_run = 0.f;
   const float c = dm.c;
+  f32x16 sc[2];    // S^T of the current tile (MFMA phase -> softmax phase)
+  u32x4 pk[2][2];  // P^T operands (softmax phase -> next MFMA phase)
 
-  VRegs<D> R;
-  if (ntiles > 0) {
-    issue_k_dma<D>(smem0, rk, 0u, kssb, koff, wave);
-    load_v_regs<D>(R, rv, 0u, vssb, voff);
-    store_v_lds<D>(smem0, R, t);
+  auto kstage = [&](auto s3) -> char* {
+    constexpr int S3 = decltype(s3)::value;
+    return S3 == 0 ? sk0 : (S3 == 1 ? sk1 : sk2);
+  };
+  auto vstage = [&](auto s3) -> char* {
+    constexpr int S3 = decltype(s3)::value;
+    return S3 == 0 ? sv0 : (S3 == 1 ? sv1 : sv2);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using BT = std::true_type;
+  using BF = std::false_type;
+
+  // Prologue: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1) of stage 2.
+  if (grp == 0) {
+    issue_tile_dma<D>(sk0, rk, 0u, kssb, koff, gw);
+    issue_tile_dma<D>(sk1, rk, (uint32_t)ST::kKeys * kssb, kssb, koff, gw);
+  } else {
+    issue_tile_dma<D>(sv1, rv, 0u, vssb, voff, gw);
+    issue_tile_dma<D>(sv2, rv, (uint32_t)ST::kKeys * vssb, vssb, voff, gw);
   }
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // these loads and Q
+  phase_barrier();
+  if (grp == 1) phase_barrier();  // group B runs one phase behind
 
-  auto step = [&](auto bufc, int it) {
-    constexpr int BUF = decltype(bufc)::value;
-    const char* cur = BUF ? smem1 : smem0;
-    char* nxt = BUF ? smem0 : smem1;
-    const int key0 = it * FT::kKeys;
-    const bool has_next = it + 1 < ntiles;
-    if (has_next) {
-      const uint32_t k1 = (uint32_t)(key0 + FT::kKeys);
-      issue_k_dma<D>(nxt, rk, k1 * kssb, kssb, koff, wave);
-      load_v_regs<D>(R, rv, k1 * vssb, vssb, voff);
-    }
+  // MFMA phase tt: P*V of tile tt-1 and S^T of tile tt, from stage tt (ring
+  // slot tt % 3).
+  auto mphase = [&](auto s3, auto pvc, auto sc_, int tt) {
+    constexpr bool DO_PV = decltype(pvc)::value;
+    constexpr bool DO_S = decltype(sc_)::value;
+    constexpr int NPV = DO_PV ? 4 * NDB : 0;
+    constexpr int NS = DO_S ? 2 * NKS : 0;
+    const char* ck = kstage(s3);
+    const char* cv = vstage(s3);
     __builtin_amdgcn_sched_barrier(0);
-
-    // S^T = K Q^T for the two 32-key blocks, the chains interleaved and each
-    // K operand read from LDS four MFMAs ahead of its use.
-    f32x16 sc[2];
-    sc[0] = f32x16{};
-    sc[1] = f32x16{};
-    {
-      u32x4 ak[D / 16][2];
+    u32x4 opv[NPV > 0 ? NPV : 1];
+    u32x4 opk[NS > 0 ? NS : 1];
+    if constexpr (DO_PV) {
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-          ak[ks][mb] = *reinterpret_cast<const u32x4*>(cur + mb * 32 * (2 * D) + ka[ks]);
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) sc[mb] = E::mfma(ak[ks][mb], qreg[ks], sc[mb]);
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 LDS reads
-#pragma unroll
-      for (int j = 0; j < D / 8 - 4; ++j) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      for (int j = 0; j < NPV; ++j) {
+        const int mb = j / (2 * NDB), kk = (j / NDB) & 1, db = j % NDB;
+        const int ro = (32 * mb + 16 * kk) * (2 * D);
+        const u32x2 lo = ld_tr(cv + vb[db] + ro);
+        const u32x2 hi = ld_tr(cv + vb[db] + ro + 4 * (2 * D));
+        opv[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // last 4 MFMAs
     }
+    if constexpr (DO_S) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + ka[j >> 1]);
+    }
+    if constexpr (DO_PV) {
+#pragma unroll
+      for (int j = 0; j < NPV; ++j) {
+        const int mb = j / (2 * NDB), kk = (j / NDB) & 1, db = j % NDB;
+        acc[db] = E::mfma(opv[j], pk[mb][kk], acc[db]);
+      }
+    }
+    if constexpr (DO_S) {
+      sc[0] = f32x16{};
+      sc[1] = f32x16{};
+#pragma unroll
+      for (int j = 0; j < NS; ++j) sc[j & 1] = E::mfma(opk[j], qreg[j >> 1], sc[j & 1]);
+    }
+    mphase_prefetch<NPV, NPV + NS, PF, 0>();
+    mphase_pipe<NPV, NPV + NS, PF, 0>();
+    if constexpr (DO_S) {
+      pin(sc[0]);
+      pin(sc[1]);
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) pin(acc[db]);
+    phase_barrier();
+  };
 
-    const bool need_mask = (key0 + FT::kKeys > dm.Skv) || (dm.causal && key0 + FT::kKeys - 1 > qpos_lo);
+  // Softmax phase of tile tt (ring slot tt % 3).  First issues this wave's
+  // share of the loads two tiles ahead (group A: K(tt+2) into stage tt+2;
+  // group B: V(tt+2) into stage tt+3), last waits for the loads it issued one
+  // softmax phase earlier.
+  auto vphase = [&](auto s3, int tt) {
+    constexpr int S3 = decltype(s3)::value;
+    if (grp == 0) {
+      issue_tile_dma<D>(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), rk,
+                        (uint32_t)((tt + 2) * ST::kKeys) * kssb, kssb, koff, gw);
+    } else {
+      issue_tile_dma<D>(vstage(s3), rv, (uint32_t)((tt + 2) * ST::kKeys) * vssb, vssb, voff, gw);
+    }
+    const int key0 = tt * ST::kKeys;
+    const bool need_mask = (key0 + ST::kKeys > dm.Skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
     if (need_mask) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
@@ -177,31 +425,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
     }
-    const float nmc = softmax_rescale<D / 32>(sc, m_run, l_run, acc, c);
-    // P of block 0 feeds its PV MFMAs while block 1 is exponentiated.
+    const float nmc = softmax_rescale<NDB>(sc, m_run, l_run, acc, c);
+    const float rs0 = softmax_exp<DT>(sc[0], nmc, c, pk[0]);
+    const float rs1 = softmax_exp<DT>(sc[1], nmc, c, pk[1]);
+    l_run += rs0 + rs1;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      u32x4 pk[2];
-      softmax_exp<DT>(sc[mb], nmc, l_run, c, pk);
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+      for (int kk = 0; kk < 2; ++kk) pin(pk[mb][kk]);
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(cur + 4096 * db + va[mb ^ (db & 1)][kk]);
-          acc[db] = E::mfma(a, pk[kk], acc[db]);
-        }
-    }
-
-    if (has_next) store_v_lds<D>(nxt, R, t);
-    __syncthreads();
+    for (int db = 0; db < NDB; ++db) pin(acc[db]);
+    pin(l_run);
+    pin(m_run);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(ST::NI));  // all but this phase's loads
+    phase_barrier();
   };
 
-  int it = 0;
-  for (; it + 2 <= ntiles; it += 2) {
-    step(std::integral_constant<int, 0>{}, it);
-    step(std::integral_constant<int, 1>{}, it + 1);
+  if (ntiles > 0) {
+    mphase(I0{}, BF{}, BT{}, 0);
+    vphase(I0{}, 0);
+    int tt = 1;
+    for (; tt + 3 <= ntiles; tt += 3) {
+      mphase(I1{}, BT{}, BT{}, tt);
+      vphase(I1{}, tt);
+      mphase(I2{}, BT{}, BT{}, tt + 1);
+      vphase(I2{}, tt + 1);
+      mphase(I0{}, BT{}, BT{}, tt + 2);
+      vphase(I0{}, tt + 2);
+    }
+    if (tt < ntiles) {
+      mphase(I1{}, BT{}, BT{}, tt);
+      vphase(I1{}, tt);
+      ++tt;
+      if (tt < ntiles) {
+        mphase(I2{}, BT{}, BT{}, tt);
+        vphase(I2{}, tt);
+        ++tt;
+      }
+    }
+    const int s3 = tt % 3;
+    if (s3 == 0) mphase(I0{}, BT{}, BF{}, tt);
+    else if (s3 == 1) mphase(I1{}, BT{}, BF{}, tt);
+    else mphase(I2{}, BT{}, BF{}, tt);
+  } else {
+    phase_barrier();
   }
-  if (it < ntiles) step(std::integral_constant<int, 0>{}, it);
+  if (grp == 0) phase_barrier();  // both groups pass the same number of barriers
+  // No LDS-DMA load (of a tile past the end) may still be writing when the
+  // workgroup exits.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // Epilogue: o = acc / l (0/0 = NaN for a row with no visible key, as the
   // reference's acc / l_i at gqa_fwd.py:106).
@@ -211,7 +483,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb +
               (int64_t)head * p.o.sh + (int64_t)pos * p.o.ss;
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         u32x2 x;
@@ -226,7 +498,7 @@ template <int DT, int D>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   const int total = p.n_mblk * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D>), dim3(total), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D>), dim3(total), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();
 }
 

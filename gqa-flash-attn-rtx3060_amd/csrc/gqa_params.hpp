@@ -23,7 +23,7 @@ struct Dims {
 struct FwdParams {
   TensorRef q, k, v, o;
   Dims dm;
-  int block_m;  // query positions per workgroup (G * block_m <= 128 packed rows)
+  int block_m;  // query positions per workgroup (G * block_m <= kFwdRows packed rows)
   int n_mblk;   // ceil(Sq / block_m)
 };
 
@@ -53,8 +53,9 @@ struct ReduceParams {
   int B, Hq, Sq, D, splits;
 };
 
-// Packed query rows per single-pass workgroup (4 waves x 32 rows).
-constexpr int kFwdRows = 128;
+// Packed query rows per single-pass workgroup (8 waves x 32 rows).
+constexpr int kFwdRows = 256;
+constexpr int kFwdThreads = 512;
 // Keys per single-pass LDS tile, and per split-KV LDS tile.
 constexpr int kFwdTileKeys = 64;
 constexpr int kSplitTileKeys = 128;

@@ -22,7 +22,7 @@ __all__ = ["gqa_flash_attn", "Route", "choose_route"]
 LOG2E = math.log2(math.e)
 
 # Packed query rows of one single-pass workgroup, and of one split-KV row block.
-FWD_ROWS = 128
+FWD_ROWS = 256
 SPLIT_ROWS = 32
 # The split-KV path is taken for at most this many packed rows per kv head.
 SPLIT_MAX_ROWS = 64

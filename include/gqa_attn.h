@@ -41,7 +41,8 @@ extern "C" {
 #define GQA_E_SHAPE (-1)      /* non-positive size or num_heads % num_kv_heads != 0 */
 #define GQA_E_HEAD_DIM (-2)   /* head_dim not in {64, 128} (dispatch.py:32) */
 #define GQA_E_DTYPE (-3)      /* dtype code not GQA_DTYPE_BF16 / GQA_DTYPE_FP16 */
-#define GQA_E_STRIDE (-4)     /* last-dim stride != 1 or rows not 16-byte aligned */
+#define GQA_E_STRIDE (-4)     /* last-dim stride != 1, rows not 16-byte aligned, or (single
+                                 pass) (seq_kv + 192) * row stride * 2 bytes >= 2^31 */
 #define GQA_E_SPLITS (-5)     /* splits outside [1, GQA_MAX_SPLITS] */
 #define GQA_E_GROUP (-6)      /* group size above what one packed tile holds */
 #define GQA_E_NULL (-7)       /* null pointer argument */

@@ -81,7 +81,7 @@ _FAKE = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced: validation fail
     (dict(D=96), -2),               # head_dim
     (dict(dtype=7), -3),            # dtype
     (dict(stride=_BAD), -4),        # last-dim stride
-    (dict(Hq=256, Hkv=1), -6),      # group larger than one packed tile
+    (dict(Hq=512, Hkv=1), -6),      # group larger than one packed tile
     (dict(Sq=-1), -1),
 ])
 def test_fwd_launch_validation(lib, args, code):
@@ -91,6 +91,23 @@ def test_fwd_launch_validation(lib, args, code):
     rc = lib.gqa_fwd_launch(_FAKE, st, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4,
                             1, p["Hq"], p["Hkv"], p["Sq"], 128, p["D"], 0.1275, 1, p["dtype"], None)
     assert rc == code
+
+
+def test_fwd_launch_rejects_rows_beyond_32bit_offsets(lib):
+    # The single-pass kernel addresses one head's K/V rows with 32-bit byte
+    # offsets up to two 64-key tiles past the end: (seq_kv + 192) * row
+    # stride * 2 must stay below 2^31.
+    # Rows of 2^21 bytes: seq_kv + 192 must stay below 1024, so 832 keys are
+    # the first rejected length.  (Only rejected calls: a call that passes
+    # validation would launch on these fake pointers.)
+    ss = 1 << 20
+    big = (ctypes.c_int64 * 4)(8 * 1024 * ss, 1024 * ss, ss, 1)
+    args = lambda kst, vst, skv: (_FAKE, _S4, _FAKE, kst, _FAKE, vst, _FAKE, _S4,
+                                  1, 32, 8, 128, skv, 128, 0.1275, 1, 0, None)
+    assert lib.gqa_fwd_launch(*args(big, big, 832)) == -4
+    assert lib.gqa_fwd_launch(*args(big, big, 1 << 20)) == -4
+    assert lib.gqa_fwd_launch(*args(_S4, big, 832)) == -4  # V alone too long
+    assert lib.gqa_fwd_launch(*args(big, _S4, 832)) == -4  # K alone too long
 
 
 def test_empty_launches_are_noops(lib):
@@ -139,9 +156,9 @@ def test_split_launch_validation(lib):
 def test_route_baseline_configs():
     from gqa_kernels.dispatch import choose_route
     cu = 256
-    # prefill: single pass, 128 packed rows (32 positions x 4 heads) per workgroup
+    # prefill: single pass, 256 packed rows (64 positions x 4 heads) per workgroup
     r = choose_route(1, 32, 8, 16384, 16384, cu)
-    assert r.kind == "single" and r.workgroups == 512 * 8
+    assert r.kind == "single" and r.workgroups == 256 * 8
     # decode 131072: split to 2 workgroups per CU
     r = choose_route(1, 32, 8, 1, 131072, cu)
     assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
