@@ -190,6 +190,37 @@ def cpu_decode_baseline(torch, budget_runs=10):
             "cores": _cpu_threads(), "config": "decode B=1 Hq=32 Hkv=8 D=128 Sq=1 Skv=2048"}
 
 
+TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
+
+
+def _load_traffic():
+    """Measured HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE,
+    scaled by what the same counters read for a plain copy of known size),
+    recorded in profiles/hbm_traffic.json; None if absent."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+
+
+def _traffic_bytes(traffic, workload):
+    if not traffic or workload not in traffic.get("workloads", {}):
+        return None
+    return traffic["workloads"][workload]["hbm_bytes_per_call"]
+
+
+def copy_calibration(torch, steps, warmup):
+    """A plain device copy of 1 GiB (torch's copy kernel): reads and writes
+    exactly 2^30 bytes per launch, the reference point for the HBM traffic
+    counters."""
+    n = 1 << 28  # fp32 elements = 1 GiB
+    src = torch.empty(n, dtype=torch.float32, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    ms = _time(torch, lambda i: dst.copy_(src), steps, warmup)
+    return {"workload": "copy 1 GiB fp32 (calibration)", "bytes_read": 4 * n, "bytes_written": 4 * n,
+            "ms": ms, "gbs": 8 * n / (ms * 1e-3) / 1e9}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,8 +228,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
     ap.add_argument("--sweep", action="store_true", help="also time every BASELINE config")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
-                    help="time one workload only (for profiling runs)")
+    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+                    help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
+                         "device copy, the calibration kernel of the HBM traffic counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -224,6 +256,12 @@ def main() -> int:
                    "global_batch": B, "seq_len": PREFILL_S, "parallelism": "single GPU"},
     }
 
+    if args.only == "copy":
+        print(json.dumps(copy_calibration(torch, args.steps, args.warmup)))
+        return 0
+
+    traffic = _load_traffic()
+
     # ---------------- prefill (headline) ----------------
     if args.only in (None, "prefill"):
         q, kvs = _inputs(torch, B, HQ, HKV, PREFILL_S, PREFILL_S, D)
@@ -240,8 +278,10 @@ def main() -> int:
         result["roofline"] = {
             "bound": "mfma", "kernel": "gqa_fwd_kernel", "achieved": tflops,
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS,
-            "traffic": None, "flops_per_launch": fl,
-            "note": "achieved = algorithmic FLOPs per launch / mean launch time (one launch per step)",
+            "traffic": _traffic_bytes(traffic, "prefill"), "flops_per_launch": fl,
+            "note": "achieved = algorithmic FLOPs per launch / mean launch time (one launch per step); "
+                    "traffic = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                    "calibrated on a plain copy (" + TRAFFIC_FILE.name + ")",
         }
         if not args.skip_cpu:
             result["cpu_baseline"] = cpu_baseline(torch, q, k, v)
@@ -264,7 +304,9 @@ def main() -> int:
             "us": ms * 1e3, "gbs": gbs, "steps": dsteps, "splits": route.splits,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": gbs / PEAK_HBM_GBS, "bytes_per_call": by,
-                         "note": "whole call (split first pass + combine), 2 rotating K/V sets"},
+                         "traffic": _traffic_bytes(traffic, "decode"),
+                         "note": "whole call (split first pass + combine), 2 rotating K/V sets; "
+                                 "traffic = measured HBM bytes per call (" + TRAFFIC_FILE.name + ")"},
         }
         if not args.skip_cpu:
             result["decode"]["cpu_baseline"] = cpu_decode_baseline(torch)
