@@ -8,6 +8,7 @@ HIP kernels through the C ABI of libgqa_hip.so.
 """
 from __future__ import annotations
 
+import contextlib
 import functools
 import math
 from dataclasses import dataclass
@@ -75,6 +76,9 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     return Route("single", 1, single_wgs)
 
 
+_route_cached = functools.lru_cache(maxsize=4096)(choose_route)
+
+
 @functools.lru_cache(maxsize=None)
 def _cu_count(device_index: int) -> int:
     n = _lib.load().gqa_device_cu_count(device_index)
@@ -119,9 +123,10 @@ def gqa_flash_attn(q, k, v, causal=True):
     q_in = q
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
-    route = choose_route(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev))
+    route = _route_cached(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev))
 
-    with torch.cuda.device(dev):
+    # Launch on q's device (a no-op context when it is already current).
+    with torch.cuda.device(dev) if dev != torch.cuda.current_device() else contextlib.nullcontext():
         if route.kind == "split":
             return split_kv_forward(q, k, v, causal, route.splits)
 

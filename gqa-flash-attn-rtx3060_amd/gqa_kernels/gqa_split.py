@@ -24,6 +24,23 @@ __all__ = ["split_kv_forward", "workspace_bytes"]
 _counters: dict = {}
 _counters_lock = threading.Lock()
 
+# fp32 split workspaces, one per (device, stream), grown on demand: a call's
+# partials are dead once its combine has run, and calls on one stream run in
+# order, so every call on that stream can reuse one buffer.  (The caching
+# allocator would hand out the same memory anyway; keeping it saves the
+# allocation on every decode step.)
+_workspaces: dict = {}
+
+
+def _workspace_buffer(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream)
+    with _counters_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() * 4 < nbytes:
+            buf = torch.empty(max(nbytes // 4, 1 << 16), dtype=torch.float32, device=device)
+            _workspaces[key] = buf
+        return buf
+
 
 def _counter_buffer(device: torch.device, stream: int, n: int) -> torch.Tensor:
     key = (device.index, stream)
@@ -54,7 +71,8 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False):
     fused combine of the last workgroup sits on the critical path).
 
     ``workspace`` may be a caller-provided fp32 CUDA tensor with at least
-    ``workspace_bytes(...) / 4`` elements; otherwise one is allocated.
+    ``workspace_bytes(...) / 4`` elements; otherwise the stream's cached
+    workspace is used (grown when too small).
     """
     lib = _lib.load()
     batch, num_heads, seq_q, head_dim = q.shape
@@ -63,15 +81,14 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False):
     dtype = _DTYPES[q.dtype]
 
     need = workspace_bytes(batch, num_heads, seq_q, head_dim, splits)
-    assert need == lib.gqa_split_workspace_bytes(batch, num_heads, seq_q, head_dim, splits)
+    stream = torch.cuda.current_stream(q.device).cuda_stream
     if workspace is None:
-        workspace = torch.empty(need // 4, dtype=torch.float32, device=q.device)
+        workspace = _workspace_buffer(q.device, stream, need)
     else:
         assert workspace.dtype == torch.float32 and workspace.device == q.device
         assert workspace.numel() * 4 >= need, "workspace too small"
     o = torch.empty_like(q)
 
-    stream = torch.cuda.current_stream(q.device).cuda_stream
     group = num_heads // num_kv_heads
     if fused and min(32, group * seq_q) * splits <= FUSED_MAX_ROW_SPLITS:
         n = lib.gqa_split_counters_count(batch, num_heads, num_kv_heads, seq_q)
