@@ -16,7 +16,7 @@ namespace {
 using gqa::Dims;
 using gqa::TensorRef;
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -84,10 +84,14 @@ size_t gqa_split_workspace_bytes(int batch, int num_heads, int seq_q, int head_d
   return rows * ((size_t)head_dim + 2) * sizeof(float);
 }
 
-int gqa_fwd_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
-                   const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], int batch,
-                   int num_heads, int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2,
-                   int causal, int dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int fwd_impl(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4], const void* v,
+             const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse, int batch, int num_heads,
+             int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2, int causal, int dtype,
+             void* stream) {
   int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
   if (rc) return rc;
   const int G = num_heads / num_kv_heads;
@@ -105,7 +109,35 @@ int gqa_fwd_launch(const void* q, const int64_t q_stride[4], const void* k, cons
   p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, G, scale_log2, causal ? 1 : 0};
   p.block_m = gqa::kFwdRows / G;
   p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  p.lse = lse;
   return to_code(gqa::launch_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int check_lse(const float* lse) {
+  if (lse == nullptr) return GQA_E_NULL;
+  return (reinterpret_cast<uintptr_t>(lse) & 3u) != 0 ? GQA_E_STRIDE : GQA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gqa_fwd_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                   const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], int batch,
+                   int num_heads, int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2,
+                   int causal, int dtype, void* stream) {
+  return fwd_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, nullptr, batch, num_heads, num_kv_heads,
+                  seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
+}
+
+int gqa_fwd_lse_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                       const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse,
+                       int batch, int num_heads, int num_kv_heads, int seq_q, int seq_kv, int head_dim,
+                       float scale_log2, int causal, int dtype, void* stream) {
+  const int rc = check_lse(lse);
+  if (rc && batch > 0 && seq_q > 0) return rc;
+  return fwd_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, batch, num_heads, num_kv_heads,
+                  seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
 }
 
 int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
@@ -136,6 +168,7 @@ int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void*
   p.n_rblk = (G * seq_q + 31) / 32;
   p.counters = nullptr;
   p.o = TensorRef{nullptr, 0, 0, 0};
+  p.lse = nullptr;
   return to_code(gqa::launch_split_first(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
@@ -145,11 +178,14 @@ size_t gqa_split_counters_count(int batch, int num_heads, int num_kv_heads, int 
   return (size_t)batch * num_kv_heads * ((G * seq_q + 31) / 32);
 }
 
-int gqa_split_fused_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
-                           const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
-                           float* workspace, int* counters, int splits, int batch, int num_heads,
-                           int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2, int causal,
-                           int dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int fused_impl(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+               const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse,
+               float* workspace, int* counters, int splits, int batch, int num_heads, int num_kv_heads,
+               int seq_q, int seq_kv, int head_dim, float scale_log2, int causal, int dtype, void* stream) {
   int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
   if (rc) return rc;
   if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
@@ -177,11 +213,56 @@ int gqa_split_fused_launch(const void* q, const int64_t q_stride[4], const void*
   p.n_rblk = (G * seq_q + 31) / 32;
   p.counters = counters;
   p.o = ref(o, o_stride);
+  p.lse = lse;
   return to_code(gqa::launch_split_first(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_stride[4], float* lse, int batch,
+                int num_heads, int seq_q, int head_dim, int dtype, void* stream);
+
+}  // namespace
+
+extern "C" {
+
+int gqa_split_fused_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                           const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
+                           float* workspace, int* counters, int splits, int batch, int num_heads,
+                           int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2, int causal,
+                           int dtype, void* stream) {
+  return fused_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, nullptr, workspace, counters, splits,
+                    batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
+}
+
+int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4], const void* k,
+                               const int64_t k_stride[4], const void* v, const int64_t v_stride[4], void* o,
+                               const int64_t o_stride[4], float* lse, float* workspace, int* counters, int splits,
+                               int batch, int num_heads, int num_kv_heads, int seq_q, int seq_kv, int head_dim,
+                               float scale_log2, int causal, int dtype, void* stream) {
+  const int rc = check_lse(lse);
+  if (rc && batch > 0 && seq_q > 0) return rc;
+  return fused_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, workspace, counters, splits, batch,
+                    num_heads, num_kv_heads, seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
 }
 
 int gqa_split_reduce_launch(const float* workspace, int splits, void* o, const int64_t o_stride[4], int batch,
                             int num_heads, int seq_q, int head_dim, int dtype, void* stream) {
+  return reduce_impl(workspace, splits, o, o_stride, nullptr, batch, num_heads, seq_q, head_dim, dtype, stream);
+}
+
+int gqa_split_reduce_lse_launch(const float* workspace, int splits, void* o, const int64_t o_stride[4],
+                                float* lse, int batch, int num_heads, int seq_q, int head_dim, int dtype,
+                                void* stream) {
+  const int rc = check_lse(lse);
+  if (rc && batch > 0 && seq_q > 0) return rc;
+  return reduce_impl(workspace, splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_stride[4], float* lse, int batch,
+                int num_heads, int seq_q, int head_dim, int dtype, void* stream) {
   if (batch < 0 || num_heads <= 0 || seq_q < 0) return GQA_E_SHAPE;
   if (head_dim != 64 && head_dim != 128) return GQA_E_HEAD_DIM;
   if (dtype != GQA_DTYPE_BF16 && dtype != GQA_DTYPE_FP16) return GQA_E_DTYPE;
@@ -202,7 +283,8 @@ int gqa_split_reduce_launch(const float* workspace, int splits, void* o, const i
   p.Sq = seq_q;
   p.D = head_dim;
   p.splits = splits;
+  p.lse = lse;
   return to_code(gqa::launch_split_reduce(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
-}  // extern "C"
+}  // namespace

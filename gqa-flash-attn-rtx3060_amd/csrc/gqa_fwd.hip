@@ -476,9 +476,13 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // Epilogue: o = acc / l (0/0 = NaN for a row with no visible key, as the
-  // reference's acc / l_i at gqa_fwd.py:106).
+  // reference's acc / l_i at gqa_fwd.py:106).  Optional LSE side output:
+  // ln sum_k exp(s_k * D^-0.5) = (m_ref * c + log2 l) * ln 2 (l is relative
+  // to the reference point m_ref); -inf for a row with no visible key.
   const float l_tot = xhalf_sum(l_run);
   const float inv = 1.0f / l_tot;
+  if (p.lse != nullptr && valid && hh == 0)
+    p.lse[((int64_t)b * dm.Hq + head) * dm.Sq + pos] = (m_run * c + __log2f(l_tot)) * kLn2;
   if (valid) {
     T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb +
               (int64_t)head * p.o.sh + (int64_t)pos * p.o.ss;

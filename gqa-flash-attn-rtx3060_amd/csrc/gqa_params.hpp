@@ -25,6 +25,7 @@ struct FwdParams {
   Dims dm;
   int block_m;  // query positions per workgroup (G * block_m <= kFwdRows packed rows)
   int n_mblk;   // ceil(Sq / block_m)
+  float* lse;   // optional (nullptr): natural-log LSE per row, contiguous (B, Hq, Sq)
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).
@@ -42,6 +43,7 @@ struct SplitParams {
   // counters: B * Hkv * n_rblk ints, zero on entry, left zero on exit.
   int* counters;
   TensorRef o;
+  float* lse;  // optional, fused combine only: as FwdParams::lse
 };
 
 // Split-KV combine: one workgroup per (b, q head, query row).
@@ -51,11 +53,14 @@ struct ReduceParams {
   const float* ws_l;
   TensorRef o;
   int B, Hq, Sq, D, splits;
+  float* lse;  // optional: as FwdParams::lse
 };
 
 // Packed query rows per single-pass workgroup (8 waves x 32 rows).
 constexpr int kFwdRows = 256;
 constexpr int kFwdThreads = 512;
+// ln(2): converts a log2-domain log-sum-exp to the natural-log LSE.
+constexpr float kLn2 = 0.693147180559945309f;
 // Keys per single-pass LDS tile, and per split-KV LDS tile.
 constexpr int kFwdTileKeys = 64;
 constexpr int kSplitTileKeys = 128;

@@ -77,6 +77,7 @@ __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb
     float l = 0.f;
     for (int sp = 0; sp < S; ++sp) l += ma[t * S + sp] * la[t * S + sp];
     lst[t] = l;
+    if (p.lse != nullptr) p.lse[row_index(t) / S] = (mst[t] + __log2f(l)) * kLn2;
   }
 
   // Split groups: enough work items (<= 1024) to keep many loads in flight.
@@ -362,6 +363,8 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
     const int pos = row % p.Sq;
     const int bh = row / p.Sq;
     const int h = bh % p.Hq, b = bh / p.Hq;
+    // Optional LSE side output (natural log; m* and l* are log2-domain).
+    if (p.lse != nullptr && d4 == 0) p.lse[row] = (mstar + __log2f(l)) * kLn2;
     T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh +
               (int64_t)pos * p.o.ss;
     u32x2 x;

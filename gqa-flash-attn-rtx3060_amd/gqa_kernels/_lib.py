@@ -17,7 +17,7 @@ DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 
 GQA_MAX_SPLITS = 1024
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64x4 = ctypes.c_int64 * 4
 _p = ctypes.c_void_p
@@ -39,6 +39,16 @@ SIGNATURES = {
         [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
     ),
     "gqa_split_reduce_launch": (_i, [_p, _i, _p, _i64x4, _i, _i, _i, _i, _i, _p]),
+    "gqa_fwd_lse_launch": (
+        _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
+    "gqa_split_reduce_lse_launch": (_i, [_p, _i, _p, _i64x4, _p, _i, _i, _i, _i, _i, _p]),
+    "gqa_split_fused_lse_launch": (
+        _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _p, _p, _i,
+         _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
     "gqa_split_counters_count": (ctypes.c_size_t, [_i, _i, _i, _i]),
     "gqa_split_fused_launch": (
         _i,

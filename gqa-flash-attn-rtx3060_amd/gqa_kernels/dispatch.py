@@ -95,7 +95,7 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
-def gqa_flash_attn(q, k, v, causal=True):
+def gqa_flash_attn(q, k, v, causal=True, *, return_lse=False):
     """GQA flash attention.
 
     Args:
@@ -106,8 +106,16 @@ def gqa_flash_attn(q, k, v, causal=True):
                 attends to K positions [0, q_pos]. Works for prefill
                 (seq_q == seq_kv) and decode / chunked-prefill (seq_q < seq_kv).
 
+        return_lse: (keyword-only extension, not in the reference) also return
+                the natural-log log-sum-exp of the scaled scores of every
+                query row, fp32 (batch, num_heads, seq_q); -inf for a row
+                with no visible key.  Two attention outputs over disjoint key
+                ranges merge exactly with it (context-parallel / ring
+                attention, prefix-cache composition).
+
     Returns:
-        (batch, num_heads, seq_q, head_dim), same dtype as q.
+        (batch, num_heads, seq_q, head_dim), same dtype as q; with
+        return_lse=True the pair (o, lse).
     """
     batch, num_heads, seq_q, head_dim = q.shape
     _, num_kv_heads, seq_kv, _ = k.shape
@@ -128,7 +136,7 @@ def gqa_flash_attn(q, k, v, causal=True):
     # Launch on q's device (a no-op context when it is already current).
     with torch.cuda.device(dev) if dev != torch.cuda.current_device() else contextlib.nullcontext():
         if route.kind == "split":
-            return split_kv_forward(q, k, v, causal, route.splits)
+            return split_kv_forward(q, k, v, causal, route.splits, return_lse=return_lse)
 
         lib = _lib.load()
         o = torch.empty_like(q_in)  # as dispatch.py:47; contiguous if unusable
@@ -136,14 +144,13 @@ def gqa_flash_attn(q, k, v, causal=True):
             o = torch.empty_like(q_in, memory_format=torch.contiguous_format)
         scale_log2 = (head_dim ** -0.5) * LOG2E
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        _lib.check(
-            lib.gqa_fwd_launch(
-                q.data_ptr(), _lib.strides(q),
-                k.data_ptr(), _lib.strides(k),
-                v.data_ptr(), _lib.strides(v),
-                o.data_ptr(), _lib.strides(o),
-                batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
-                scale_log2, int(bool(causal)), _DTYPES[q.dtype], stream,
-            )
-        )
-        return o
+        common = (batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
+                  scale_log2, int(bool(causal)), _DTYPES[q.dtype], stream)
+        qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),
+                v.data_ptr(), _lib.strides(v), o.data_ptr(), _lib.strides(o))
+        if not return_lse:
+            _lib.check(lib.gqa_fwd_launch(*qkvo, *common))
+            return o
+        lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device)
+        _lib.check(lib.gqa_fwd_lse_launch(*qkvo, lse.data_ptr(), *common))
+        return o, lse

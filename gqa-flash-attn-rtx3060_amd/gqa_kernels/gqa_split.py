@@ -64,11 +64,14 @@ def workspace_bytes(batch: int, num_heads: int, seq_q: int, head_dim: int, split
     return batch * num_heads * seq_q * splits * (head_dim + 2) * 4
 
 
-def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False):
+def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False, return_lse=False):
     """Split-KV forward: first pass over `splits` chunks of the keys, then the
     log-sum-exp combine (a second launch, or fused into the first pass with
     ``fused=True``; the two-launch form measured faster on MI355X because the
     fused combine of the last workgroup sits on the critical path).
+
+    ``return_lse`` also returns the natural-log LSE per query row, fp32
+    (B, Hq, Sq), computed by the combine; the result is then ``(o, lse)``.
 
     ``workspace`` may be a caller-provided fp32 CUDA tensor with at least
     ``workspace_bytes(...) / 4`` elements; otherwise the stream's cached
@@ -88,23 +91,22 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False):
         assert workspace.dtype == torch.float32 and workspace.device == q.device
         assert workspace.numel() * 4 >= need, "workspace too small"
     o = torch.empty_like(q)
+    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
 
     group = num_heads // num_kv_heads
     if fused and min(32, group * seq_q) * splits <= FUSED_MAX_ROW_SPLITS:
         n = lib.gqa_split_counters_count(batch, num_heads, num_kv_heads, seq_q)
         counters = _counter_buffer(q.device, stream, n)
-        _lib.check(
-            lib.gqa_split_fused_launch(
-                q.data_ptr(), _lib.strides(q),
-                k.data_ptr(), _lib.strides(k),
-                v.data_ptr(), _lib.strides(v),
-                o.data_ptr(), _lib.strides(o),
-                workspace.data_ptr(), counters.data_ptr(), splits,
+        qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),
+                v.data_ptr(), _lib.strides(v), o.data_ptr(), _lib.strides(o))
+        rest = (workspace.data_ptr(), counters.data_ptr(), splits,
                 batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
-                scale_log2, int(bool(causal)), dtype, stream,
-            )
-        )
-        return o
+                scale_log2, int(bool(causal)), dtype, stream)
+        if lse is None:
+            _lib.check(lib.gqa_split_fused_launch(*qkvo, *rest))
+            return o
+        _lib.check(lib.gqa_split_fused_lse_launch(*qkvo, lse.data_ptr(), *rest))
+        return o, lse
     _lib.check(
         lib.gqa_split_first_launch(
             q.data_ptr(), _lib.strides(q),
@@ -115,11 +117,10 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False):
             scale_log2, int(bool(causal)), dtype, stream,
         )
     )
-    _lib.check(
-        lib.gqa_split_reduce_launch(
-            workspace.data_ptr(), splits,
-            o.data_ptr(), _lib.strides(o),
-            batch, num_heads, seq_q, head_dim, dtype, stream,
-        )
-    )
-    return o
+    if lse is None:
+        _lib.check(lib.gqa_split_reduce_launch(workspace.data_ptr(), splits, o.data_ptr(), _lib.strides(o),
+                                               batch, num_heads, seq_q, head_dim, dtype, stream))
+        return o
+    _lib.check(lib.gqa_split_reduce_lse_launch(workspace.data_ptr(), splits, o.data_ptr(), _lib.strides(o),
+                                               lse.data_ptr(), batch, num_heads, seq_q, head_dim, dtype, stream))
+    return o, lse

@@ -71,6 +71,25 @@ int gqa_fwd_launch(const void* q, const int64_t q_stride[4],
                    int seq_q, int seq_kv, int head_dim,
                    float scale_log2, int causal, int dtype, void* stream);
 
+/* LSE side output.  The *_lse_launch variants below also write, for every
+ * query row, lse = ln sum_k exp(scale * q.k) over the row's visible keys, as
+ * fp32 into a contiguous (batch, num_heads, seq_q) array (-inf for a row
+ * with no visible key).  The reference computes this quantity inside its
+ * split-KV combine (gqa_kernels/gqa_split.py:134-139, m + log2 l in log2
+ * units) but returns only o; it is what merging attention over separate key
+ * ranges needs (context-parallel / ring attention, prefix-cache
+ * composition, reference README.md:142-143).  lse must be non-NULL and
+ * 4-byte aligned. */
+
+/* gqa_fwd_launch plus the LSE side output. */
+int gqa_fwd_lse_launch(const void* q, const int64_t q_stride[4],
+                       const void* k, const int64_t k_stride[4],
+                       const void* v, const int64_t v_stride[4],
+                       void* o, const int64_t o_stride[4], float* lse,
+                       int batch, int num_heads, int num_kv_heads,
+                       int seq_q, int seq_kv, int head_dim,
+                       float scale_log2, int causal, int dtype, void* stream);
+
 /* Bytes of fp32 workspace the split-KV path needs for `splits` chunks:
  * acc (batch, num_heads, seq_q, splits, head_dim) followed by m and l
  * (batch, num_heads, seq_q, splits) each — the partial tensors of reference
@@ -99,6 +118,12 @@ int gqa_split_reduce_launch(const float* workspace, int splits,
                             int batch, int num_heads, int seq_q, int head_dim,
                             int dtype, void* stream);
 
+/* gqa_split_reduce_launch plus the LSE side output (see gqa_fwd_lse_launch). */
+int gqa_split_reduce_lse_launch(const float* workspace, int splits,
+                                void* o, const int64_t o_stride[4], float* lse,
+                                int batch, int num_heads, int seq_q, int head_dim,
+                                int dtype, void* stream);
+
 /* Number of int32 counters gqa_split_fused_launch needs: one per
  * (batch, kv head, block of 32 packed (position, head) rows). */
 size_t gqa_split_counters_count(int batch, int num_heads, int num_kv_heads, int seq_q);
@@ -121,6 +146,17 @@ int gqa_split_fused_launch(const void* q, const int64_t q_stride[4],
                            int seq_q, int seq_kv, int head_dim,
                            float scale_log2, int causal, int dtype,
                            void* stream);
+
+/* gqa_split_fused_launch plus the LSE side output (see gqa_fwd_lse_launch). */
+int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4],
+                               const void* k, const int64_t k_stride[4],
+                               const void* v, const int64_t v_stride[4],
+                               void* o, const int64_t o_stride[4], float* lse,
+                               float* workspace, int* counters, int splits,
+                               int batch, int num_heads, int num_kv_heads,
+                               int seq_q, int seq_kv, int head_dim,
+                               float scale_log2, int causal, int dtype,
+                               void* stream);
 
 #ifdef __cplusplus
 }

@@ -26,6 +26,12 @@ values, which for bf16/fp16 inputs are the bf16/fp16-rounded numbers):
   combine m* = max m, a = exp2(m - m*), o = sum a acc / sum a l
   (gqa_split.py:134-147).
 
+* ``gqa_lse`` — the log-sum-exp of each query row's scaled scores over its
+  visible keys, ln sum_k exp(q.k * head_dim^-0.5), natural log (the quantity
+  the reference's split combine forms in log2 units as m* + log2 l*,
+  gqa_split.py:134-139, without returning it); -inf for a row with no visible
+  key.  ``split_lse`` forms it from split partials the way that combine does.
+
 Parity pinning (tests/test_oracle.py): brute-force scalar loops at tiny
 shapes, closed forms (one-key row, constant V, constant-per-head V, uniform
 keys), invariants (chunked = last rows of prefill, decode causal = non-causal,
@@ -39,8 +45,8 @@ import math
 
 import numpy as np
 
-__all__ = ["gqa_reference", "split_partials", "split_combine", "split_kv_reference",
-           "attention_flops", "attention_bytes", "visible_pairs"]
+__all__ = ["gqa_reference", "gqa_lse", "split_partials", "split_combine", "split_kv_reference",
+           "split_lse", "attention_flops", "attention_bytes", "visible_pairs"]
 
 LOG2E = math.log2(math.e)
 
@@ -91,6 +97,36 @@ def gqa_reference(q, k, v, causal=True, *, rows=None, dtype=np.float32, row_chun
     return out
 
 
+def gqa_lse(q, k, v, causal=True, *, rows=None, dtype=np.float64, row_chunk=1024):
+    """Natural-log LSE (B, Hq, len(rows) or Sq) of the scaled scores of each
+    query row over its visible keys (max-subtracted, like the output's
+    softmax); -inf where no key is visible."""
+    q = np.asarray(q)
+    k = np.asarray(k)
+    B, Hq, Hkv, Sq, Skv, D = _shapes(q, k, np.asarray(v))
+    G = Hq // Hkv
+    scale = D ** -0.5
+    sel = np.arange(Sq) if rows is None else np.asarray(rows, dtype=np.int64)
+    out = np.full((B, Hq, len(sel)), -np.inf, dtype=dtype)
+    k_pos = np.arange(Skv)
+    if Skv == 0:
+        return out
+    for b in range(B):
+        for h in range(Hq):
+            kk = k[b, h // G].astype(dtype)
+            for r0 in range(0, len(sel), row_chunk):
+                idx = sel[r0:r0 + row_chunk]
+                s = (q[b, h, idx].astype(dtype) @ kk.T) * dtype(scale)
+                if causal:
+                    q_pos = idx + (Skv - Sq)
+                    s = np.where(q_pos[:, None] < k_pos[None, :], -np.inf, s)
+                m = s.max(axis=-1)
+                safe = np.where(np.isneginf(m), 0.0, m)
+                with np.errstate(divide="ignore"):
+                    out[b, h, r0:r0 + len(idx)] = safe + np.log(np.exp(s - safe[:, None]).sum(axis=-1))
+    return out
+
+
 def split_partials(q, k, v, causal, splits, *, dtype=np.float64):
     """Per-chunk partials (m, l, acc) of the split-KV first pass.
 
@@ -136,6 +172,15 @@ def split_combine(m, l, acc):
         lstar = (a * l).sum(axis=-1)
         o = (a[..., None] * acc).sum(axis=-2) / lstar[..., None]
     return o
+
+
+def split_lse(m, l):
+    """Natural-log LSE from split partials (m in log2 units): the combine's
+    m* + log2 sum_s exp2(m_s - m*) l_s, times ln 2."""
+    with np.errstate(invalid="ignore", divide="ignore"):
+        mstar = m.max(axis=-1, keepdims=True)
+        lstar = (np.exp2(m - mstar) * l).sum(axis=-1)
+        return (mstar[..., 0] + np.log2(lstar)) * math.log(2.0)
 
 
 def split_kv_reference(q, k, v, causal, splits, *, dtype=np.float64):

@@ -317,3 +317,89 @@ def test_planted_mistake_is_caught(mutant):
 
 def test_planted_split_mistake_is_caught():
     assert not pin_split(oracle64, split=_mut_split_chunking)
+
+
+# ---------------------------------------------------------------------------
+# LSE side output: gqa_lse / split_lse pinned by brute force, closed forms,
+# the split decomposition, torch.logsumexp, the normalisation identity, and
+# planted mistakes.
+# ---------------------------------------------------------------------------
+def _lse_inputs(seed=7, B=2, Hq=6, Hkv=2, Sq=5, Skv=9, D=16):
+    g = np.random.default_rng(seed)
+    return (g.standard_normal((B, Hq, Sq, D)), g.standard_normal((B, Hkv, Skv, D)),
+            g.standard_normal((B, Hkv, Skv, D)))
+
+
+def _lse_brute(q, k, v, causal):
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    out = np.empty((B, Hq, Sq))
+    for b in range(B):
+        for h in range(Hq):
+            for i in range(Sq):
+                terms = [math.exp(sum(q[b, h, i, d] * k[b, h // (Hq // Hkv), j, d] for d in range(D)) / math.sqrt(D))
+                         for j in range(Skv) if not causal or j <= i + Skv - Sq]
+                out[b, h, i] = math.log(sum(terms)) if terms else -math.inf
+    return out
+
+
+def test_lse_brute_force():
+    q, k, v = _lse_inputs()
+    for causal in (True, False):
+        assert np.abs(O.gqa_lse(q, k, v, causal) - _lse_brute(q, k, v, causal)).max() < 1e-12
+
+
+def test_lse_closed_forms():
+    q, k, v = _lse_inputs()
+    # q = 0: every visible score is 0, lse = ln(number of visible keys)
+    z = O.gqa_lse(np.zeros_like(q), k, v, True)
+    n_vis = np.arange(q.shape[2]) + (k.shape[2] - q.shape[2]) + 1
+    assert np.allclose(z, np.log(n_vis)[None, None, :], atol=1e-13)
+    # causal prefill row 0 sees one key: lse = q0.k0 / sqrt(D)
+    qs = q[:, :, :4]
+    ks, vs = k[:, :, :4], v[:, :, :4]
+    one = O.gqa_lse(qs, ks, vs, True)[:, :, 0]
+    want = np.einsum("bhd,bhd->bh", qs[:, :, 0], np.repeat(ks[:, :, 0], 3, axis=1)) / 4.0
+    assert np.allclose(one, want, atol=1e-13)
+    # all keys equal: lse = ln(n) + q.k / sqrt(D)
+    keq = np.repeat(k[:, :, :1], k.shape[2], axis=2)
+    e = O.gqa_lse(q, keq, v, False)
+    dot = np.einsum("bhsd,bhd->bhs", q, np.repeat(k[:, :, 0], 3, axis=1)) / 4.0
+    assert np.allclose(e, np.log(k.shape[2]) + dot, atol=1e-12)
+    # no visible key (causal, Sq > Skv): -inf
+    assert np.all(np.isneginf(O.gqa_lse(q[:, :, :5], k[:, :, :2], v[:, :, :2], True)[:, :, :3]))
+
+
+def test_lse_split_decomposition_and_torch():
+    q, k, v = _lse_inputs(seed=11, Skv=13)
+    ref = O.gqa_lse(q, k, v, True)
+    for splits in (1, 2, 3, 5, 13, 20):
+        m, l, _ = O.split_partials(q, k, v, True, splits)
+        assert np.abs(O.split_lse(m, l) - ref).max() < 1e-12
+    # torch.logsumexp over the masked, scaled scores (independent library)
+    tq, tk = torch.from_numpy(q), torch.from_numpy(k).repeat_interleave(3, dim=1)
+    s = tq @ tk.transpose(-1, -2) / 4.0
+    mask = torch.arange(13)[None, :] > (torch.arange(5)[:, None] + 8)
+    s = s.masked_fill(mask, float("-inf"))
+    assert np.abs(torch.logsumexp(s, dim=-1).numpy() - ref).max() < 1e-12
+
+
+def test_lse_normalises_the_softmax():
+    q, k, v = _lse_inputs(seed=3)
+    lse = O.gqa_lse(q, k, v, True)
+    s = np.einsum("bhsd,bhtd->bhst", q, np.repeat(k, 3, axis=1)) / 4.0
+    vis = np.arange(9)[None, :] <= (np.arange(5)[:, None] + 4)
+    tot = np.where(vis, np.exp(s - lse[..., None]), 0.0).sum(-1)
+    assert np.allclose(tot, 1.0, atol=1e-13)
+
+
+@pytest.mark.parametrize("mutant", ["log2", "noscale", "upper_left"])
+def test_planted_lse_mistake_is_caught(mutant):
+    q, k, v = _lse_inputs()
+    if mutant == "log2":
+        bad = O.gqa_lse(q, k, v, True) / math.log(2.0)
+    elif mutant == "noscale":
+        bad = O.gqa_lse(q * 4.0, k, v, True)
+    else:  # upper-left causal alignment: row i sees keys 0..i
+        bad = O.gqa_lse(q, k[:, :, :5], v[:, :, :5], True)
+    assert np.abs(bad - _lse_brute(q, k, v, True)).max() > 1e-3
