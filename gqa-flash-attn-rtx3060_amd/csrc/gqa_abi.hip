@@ -16,7 +16,7 @@ namespace {
 using gqa::Dims;
 using gqa::TensorRef;
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -65,6 +65,9 @@ const char* gqa_strerror(int code) {
     case GQA_E_SPLITS: return "splits out of range [1, GQA_MAX_SPLITS]";
     case GQA_E_GROUP: return "group size (num_heads / num_kv_heads) larger than 256";
     case GQA_E_NULL: return "null pointer argument";
+    case GQA_E_BLOCK:
+      return "paged cache: block_size must be a power of two in [1, GQA_MAX_BLOCK_SIZE] and "
+             "table_stride * block_size must cover max_seq_len";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -154,7 +157,7 @@ int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void*
   if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
 
   const int G = num_heads / num_kv_heads;
-  gqa::SplitParams p;
+  gqa::SplitParams p{};
   p.q = ref(q, q_stride);
   p.k = ref(k, k_stride);
   p.v = ref(v, v_stride);
@@ -170,6 +173,96 @@ int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void*
   p.o = TensorRef{nullptr, 0, 0, 0};
   p.lse = nullptr;
   return to_code(gqa::launch_split_first(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const void* k_cache,
+                                 const int64_t k_cache_stride[4], const void* v_cache,
+                                 const int64_t v_cache_stride[4], const int* block_table, int table_stride,
+                                 const int* seq_lens, int block_size, int max_seq_len, float* workspace,
+                                 int splits, int batch, int num_heads, int num_kv_heads, int seq_q, int head_dim,
+                                 float scale_log2, int causal, int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
+  if (rc) return rc;
+  if (block_size < 1 || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
+    return GQA_E_BLOCK;
+  if (table_stride < 0 || (int64_t)table_stride * block_size < (int64_t)max_seq_len) return GQA_E_BLOCK;
+  if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (workspace == nullptr || seq_lens == nullptr) return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || (reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0)
+    return GQA_E_STRIDE;
+  if ((rc = check_tensor(q, q_stride))) return rc;
+  if (max_seq_len > 0) {
+    if (block_table == nullptr) return GQA_E_NULL;
+    if ((reinterpret_cast<uintptr_t>(block_table) & 3u) != 0) return GQA_E_STRIDE;
+    if ((rc = check_tensor(k_cache, k_cache_stride)) || (rc = check_tensor(v_cache, v_cache_stride))) return rc;
+  }
+
+  const int G = num_heads / num_kv_heads;
+  gqa::SplitParams p{};
+  p.q = ref(q, q_stride);
+  p.k = ref(k_cache, k_cache_stride);
+  p.v = ref(v_cache, v_cache_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, G, scale_log2, causal ? 1 : 0};
+  const size_t rows = (size_t)batch * num_heads * seq_q * splits;
+  p.ws_acc = workspace;
+  p.ws_m = workspace + rows * head_dim;
+  p.ws_l = p.ws_m + rows;
+  p.splits = splits;
+  // Chunks start on 64-key boundaries, so with pages of 64 keys or more
+  // every full 64-key sub-tile is one strided run inside one page.
+  p.chunk = ((max_seq_len + splits - 1) / splits + 63) & ~63;
+  p.n_rblk = (G * seq_q + 31) / 32;
+  p.counters = nullptr;
+  p.o = TensorRef{nullptr, 0, 0, 0};
+  p.lse = nullptr;
+  p.block_table = block_table;
+  p.seq_lens = seq_lens;
+  p.table_stride = table_stride;
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  p.block_shift = shift;
+  return to_code(gqa::launch_paged_split_first(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gqa_paged_cache_write_launch(const void* k, const int64_t k_stride[3], const void* v,
+                                 const int64_t v_stride[3], void* k_cache, const int64_t k_cache_stride[4],
+                                 void* v_cache, const int64_t v_cache_stride[4], const int64_t* slot_mapping,
+                                 int num_tokens, int num_kv_heads, int head_dim, int block_size, int dtype,
+                                 void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0) return GQA_E_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return GQA_E_HEAD_DIM;
+  if (dtype != GQA_DTYPE_BF16 && dtype != GQA_DTYPE_FP16) return GQA_E_DTYPE;
+  if (block_size < 1 || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
+    return GQA_E_BLOCK;
+  if (num_tokens == 0) return GQA_OK;
+  if (slot_mapping == nullptr || k == nullptr || v == nullptr || k_stride == nullptr || v_stride == nullptr)
+    return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(slot_mapping) & 7u) != 0) return GQA_E_STRIDE;
+  for (const int64_t* st : {k_stride, v_stride})
+    if (st[2] != 1 || st[0] % 8 != 0 || st[1] % 8 != 0) return GQA_E_STRIDE;
+  if (((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0) return GQA_E_STRIDE;
+  int rc;
+  if ((rc = check_tensor(k_cache, k_cache_stride)) || (rc = check_tensor(v_cache, v_cache_stride))) return rc;
+
+  gqa::CacheWriteParams p{};
+  p.k = k;
+  p.v = v;
+  p.k_st = k_stride[0];
+  p.k_sh = k_stride[1];
+  p.v_st = v_stride[0];
+  p.v_sh = v_stride[1];
+  p.kc = ref(k_cache, k_cache_stride);
+  p.vc = ref(v_cache, v_cache_stride);
+  p.slots = slot_mapping;
+  p.n_tokens = num_tokens;
+  p.Hkv = num_kv_heads;
+  p.D = head_dim;
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  p.block_shift = shift;
+  p.elem_bytes = 2;
+  return to_code(gqa::launch_paged_cache_write(p, static_cast<hipStream_t>(stream)));
 }
 
 size_t gqa_split_counters_count(int batch, int num_heads, int num_kv_heads, int seq_q) {
@@ -199,7 +292,7 @@ int fused_impl(const void* q, const int64_t q_stride[4], const void* k, const in
   if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
 
   const int G = num_heads / num_kv_heads;
-  gqa::SplitParams p;
+  gqa::SplitParams p{};
   p.q = ref(q, q_stride);
   p.k = ref(k, k_stride);
   p.v = ref(v, v_stride);

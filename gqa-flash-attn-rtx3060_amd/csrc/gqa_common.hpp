@@ -145,25 +145,67 @@ __device__ inline u32x2 ld8(const void* p) {
   return *reinterpret_cast<const u32x2*>(p);
 }
 
+// Where the K or V row of key j of one (b, kv head) lives.
+//   Contiguous: base + j * row stride (the (B, H, S, D) tensors).
+//   Paged: a block table maps key j to slot j % block_size of block
+//   table[j / block_size] of a cache laid out (num_blocks, block_size,
+//   heads, D) in any strides; block_size is a power of two.
+// run64(key0): keys [key0, key0 + 64) form one strided run, so the first
+// row's address and the row stride locate all 64.  With pages of >= 64 keys
+// this holds for every 64-aligned key0 (the paged first pass starts its
+// chunks on 64-key boundaries); with smaller pages every row resolves its own
+// page.  The two paged cases are separate types so each kernel instantiation
+// carries only one load path.
+template <typename T>
+struct ContigRows {
+  const T* base;  // key 0 of this (b, kv head)
+  int64_t ss;     // key stride (elements)
+  __device__ const T* row(int key) const { return base + (int64_t)key * ss; }
+  __device__ static constexpr bool run64() { return true; }
+};
+template <typename T, bool kBigPages>
+struct PagedRows {
+  const T* base;      // the cache at this kv head (block 0, slot 0)
+  const int* table;   // this sequence's row of the block table
+  int64_t sblk, sss;  // block and slot strides (elements)
+  int shift;          // log2(block_size)
+  __device__ const T* row(int key) const {
+    return base + (int64_t)table[key >> shift] * sblk + (int64_t)(key & ((1 << shift) - 1)) * sss;
+  }
+  __device__ static constexpr bool run64() { return kBigPages; }
+};
+
 // Load keys [key0, key0 + 64) of one (b, kv head) into registers; rows at or
-// beyond `key_lim` read as zero.  kbase/vbase point at key 0 of the head;
-// kss/vss are the key strides in elements.  A tile that lies entirely below
-// key_lim (all but the last) takes the unpredicated path.
-template <int D, typename T, bool kStream = false>
-__device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kbase,
-                                    const T* __restrict__ vbase, int64_t kss, int64_t vss,
+// beyond `key_lim` read as zero.  kr/vr locate K and V rows (see run64 for
+// the alignment key0 needs).  A tile that lies entirely below key_lim (all
+// but the last) takes the unpredicated path.
+template <int D, typename T, bool kStream, typename KR>
+__device__ inline void load_subtile(SubTileRegs<D>& R, const KR& kr, const KR& vr, int64_t kss, int64_t vss,
                                     int key0, int key_lim, int t) {
   const int d4 = t % (D / 4), kg = t / (D / 4);
   constexpr int KPT = SubTileRegs<D>::KPT;
   if (key0 + 64 <= key_lim) {
+    if constexpr (KR::run64()) {
+      const T* kb = kr.row(key0);
+      const T* vb = vr.row(key0);
+#pragma unroll
+      for (int j = 0; j < SubTileRegs<D>::KCH; ++j) {
+        const int ci = t + 256 * j;
+        const int r = ci / (D / 8), cd = ci % (D / 8);
+        R.k[j] = ld16<kStream>(kb + (int64_t)r * kss + cd * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) R.v[j] = ld8<kStream>(vb + (int64_t)(kg * KPT + j) * vss + d4 * 4);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < SubTileRegs<D>::KCH; ++j) {
       const int ci = t + 256 * j;
       const int r = ci / (D / 8), cd = ci % (D / 8);
-      R.k[j] = ld16<kStream>(kbase + (int64_t)(key0 + r) * kss + cd * 8);
+      R.k[j] = ld16<kStream>(kr.row(key0 + r) + cd * 8);
     }
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) R.v[j] = ld8<kStream>(vbase + (int64_t)(key0 + kg * KPT + j) * vss + d4 * 4);
+    for (int j = 0; j < KPT; ++j) R.v[j] = ld8<kStream>(vr.row(key0 + kg * KPT + j) + d4 * 4);
     return;
   }
 #pragma unroll
@@ -172,14 +214,14 @@ __device__ inline void load_subtile(SubTileRegs<D>& R, const T* __restrict__ kba
     const int r = ci / (D / 8), cd = ci % (D / 8);
     const int key = key0 + r;
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (key < key_lim) x = ld16<kStream>(kbase + (int64_t)key * kss + cd * 8);
+    if (key < key_lim) x = ld16<kStream>(kr.row(key) + cd * 8);
     R.k[j] = x;
   }
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const int key = key0 + kg * KPT + j;
     u32x2 x = {0u, 0u};
-    if (key < key_lim) x = ld8<kStream>(vbase + (int64_t)key * vss + d4 * 4);
+    if (key < key_lim) x = ld8<kStream>(vr.row(key) + d4 * 4);
     R.v[j] = x;
   }
 }

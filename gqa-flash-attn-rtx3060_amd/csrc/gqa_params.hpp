@@ -44,6 +44,15 @@ struct SplitParams {
   int* counters;
   TensorRef o;
   float* lse;  // optional, fused combine only: as FwdParams::lse
+  // Paged K/V cache (gqa_paged_split_first_launch only): k/v point at a
+  // (num_blocks, block_size, Hkv, D) cache with sb = block stride, ss = slot
+  // stride, sh = head stride; key j of sequence b is slot j % block_size of
+  // block block_table[b * table_stride + j / block_size]; sequence b has
+  // seq_lens[b] keys (dm.Skv is the longest).
+  const int* block_table;
+  const int* seq_lens;
+  int table_stride;
+  int block_shift;  // log2(block_size)
 };
 
 // Split-KV combine: one workgroup per (b, q head, query row).
@@ -68,8 +77,22 @@ constexpr int kSplitTileKeys = 128;
 // LDS; above this the separate combine kernel is used.
 constexpr int kFusedMaxRowSplitsHost = 4096;
 
+// Paged cache write: new tokens (num_tokens, Hkv, D) into
+// (num_blocks, block_size, Hkv, D) caches at slot_mapping[t].
+struct CacheWriteParams {
+  const void* k;
+  const void* v;
+  int64_t k_st, k_sh, v_st, v_sh;  // token and head strides of k / v (elements)
+  TensorRef kc, vc;                // caches: sb = block, ss = slot, sh = head strides
+  const int64_t* slots;
+  int n_tokens, Hkv, D, block_shift;
+  int elem_bytes;
+};
+
 hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream);  // fused if p.counters
+hipError_t launch_paged_split_first(const SplitParams& p, int dtype, hipStream_t stream);
+hipError_t launch_paged_cache_write(const CacheWriteParams& p, hipStream_t stream);
 hipError_t launch_split_reduce(const ReduceParams& p, int dtype, hipStream_t stream);
 
 }  // namespace gqa

@@ -18,6 +18,16 @@
 // Combine: one workgroup per (batch, q head, row):
 //   m* = max m_s, a_s = exp2(m_s - m*), l* = sum a_s l_s,
 //   o = sum a_s acc_s / l*                         (gqa_split.py:134-147)
+//
+// Paged variants (KV = 1, 2; no counterpart in the reference): the same
+// first pass over a (num_blocks, block_size, Hkv, D) cache, with each
+// sequence's key count read from seq_lens[b] and each key row located
+// through the block table (PagedRows).  With pages of >= 64 keys (KV = 1) a
+// 64-key sub-tile is one strided run inside one page and loads like a
+// contiguous tile after one table lookup; smaller pages (KV = 2) resolve the
+// page of every row.
+#include <type_traits>
+
 #include "gqa_common.hpp"
 #include "gqa_params.hpp"
 
@@ -116,7 +126,9 @@ __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb
   }
 }
 
-template <int DT, int D>
+// KV: 0 contiguous K/V, 1 paged cache with pages of >= 64 keys, 2 paged
+// cache with smaller pages.
+template <int DT, int D, int KV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_split_first_kernel(SplitParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
@@ -141,12 +153,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kvh = rest % dm.Hkv;
   const int b = rest / dm.Hkv;
 
+  // Keys of this sequence: all of them, or (paged) its own length, clamped
+  // to [0, max_seq_len] so that no key past the block table's covered range
+  // is ever addressed.
+  constexpr bool PAGED = KV != 0;
+  const int skv = PAGED ? min(max(p.seq_lens[b], 0), dm.Skv) : dm.Skv;
+
   // This lane's query row (position-major packing).
   const int r = 32 * rb + i;
   const int pos = r / dm.G, g = r - pos * dm.G;
   const bool valid = pos < dm.Sq;
   const int head = kvh * dm.G + g;
-  const int qpos = pos + (dm.Skv - dm.Sq);
+  const int qpos = pos + (skv - dm.Sq);
 
   u32x4 qreg[D / 16];
   {
@@ -162,15 +180,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Keys of this chunk, clamped to the block's last visible key.
   const int c0 = s * p.chunk;
-  int c1 = min(c0 + p.chunk, dm.Skv);
+  int c1 = min(c0 + p.chunk, skv);
   const int pos_lo = (32 * rb) / dm.G;
   const int pos_hi = min(dm.Sq - 1, (32 * rb + 31) / dm.G);
-  if (dm.causal) c1 = min(c1, pos_hi + (dm.Skv - dm.Sq) + 1);
+  if (dm.causal) c1 = min(c1, pos_hi + (skv - dm.Sq) + 1);
   const int ntiles = c1 > c0 ? (c1 - c0 + kSplitTileKeys - 1) / kSplitTileKeys : 0;
-  const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
+  const int qpos_lo = pos_lo + (skv - dm.Sq);
 
-  const T* kbase = static_cast<const T*>(p.k.ptr) + (int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh;
-  const T* vbase = static_cast<const T*>(p.v.ptr) + (int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh;
+  using Rows = typename std::conditional<PAGED, PagedRows<T, KV == 1>, ContigRows<T>>::type;
+  Rows kr, vr;
+  if constexpr (PAGED) {
+    const int* table = p.block_table + (int64_t)b * p.table_stride;
+    kr = Rows{static_cast<const T*>(p.k.ptr) + (int64_t)kvh * p.k.sh, table, p.k.sb, p.k.ss, p.block_shift};
+    vr = Rows{static_cast<const T*>(p.v.ptr) + (int64_t)kvh * p.v.sh, table, p.v.sb, p.v.ss, p.block_shift};
+  } else {
+    kr = Rows{static_cast<const T*>(p.k.ptr) + (int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh, p.k.ss};
+    vr = Rows{static_cast<const T*>(p.v.ptr) + (int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh, p.v.ss};
+  }
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -181,8 +207,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   SubTileRegs<D> R0, R1;
   if (ntiles > 0) {
-    load_subtile<D, T, true>(R0, kbase, vbase, p.k.ss, p.v.ss, c0, c1, t);
-    load_subtile<D, T, true>(R1, kbase, vbase, p.k.ss, p.v.ss, c0 + 64, c1, t);
+    load_subtile<D, T, true>(R0, kr, vr, p.k.ss, p.v.ss, c0, c1, t);
+    load_subtile<D, T, true>(R1, kr, vr, p.k.ss, p.v.ss, c0 + 64, c1, t);
   }
   const int sub = wave >> 1, mb = wave & 1;
   const char* mytile = smem + sub * ST::kBytes;
@@ -194,8 +220,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     store_subtile<D>(smem + ST::kBytes, R1, t);
     __syncthreads();
     if (it + 1 < ntiles) {
-      load_subtile<D, T, true>(R0, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys, c1, t);
-      load_subtile<D, T, true>(R1, kbase, vbase, p.k.ss, p.v.ss, key0 + kSplitTileKeys + 64, c1, t);
+      load_subtile<D, T, true>(R0, kr, vr, p.k.ss, p.v.ss, key0 + kSplitTileKeys, c1, t);
+      load_subtile<D, T, true>(R1, kr, vr, p.k.ss, p.v.ss, key0 + kSplitTileKeys + 64, c1, t);
     }
 
     const int kb0 = key0 + 32 * wave;  // this wave's 32 keys
@@ -292,7 +318,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
 
-  if (p.counters == nullptr) return;
+  if (PAGED || p.counters == nullptr) return;
   // Fused combine: count this partial once its stores have completed, and let
   // the workgroup that completes the count for this (b, kv head, row block)
   // combine all splits.
@@ -374,11 +400,11 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   }
 }
 
-template <int DT, int D>
+template <int DT, int D, int KV>
 static hipError_t launch_split_first_t(const SplitParams& p, hipStream_t stream) {
   const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * p.n_rblk * p.splits;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_split_first_kernel<DT, D>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gqa_split_first_kernel<DT, D, KV>), dim3((unsigned)total), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -392,8 +418,20 @@ static hipError_t launch_split_reduce_t(const ReduceParams& p, hipStream_t strea
 
 hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream) {
   if (dtype == 0)
-    return p.dm.D == 128 ? launch_split_first_t<0, 128>(p, stream) : launch_split_first_t<0, 64>(p, stream);
-  return p.dm.D == 128 ? launch_split_first_t<1, 128>(p, stream) : launch_split_first_t<1, 64>(p, stream);
+    return p.dm.D == 128 ? launch_split_first_t<0, 128, 0>(p, stream) : launch_split_first_t<0, 64, 0>(p, stream);
+  return p.dm.D == 128 ? launch_split_first_t<1, 128, 0>(p, stream) : launch_split_first_t<1, 64, 0>(p, stream);
+}
+
+template <int KV>
+static hipError_t launch_paged_t(const SplitParams& p, int dtype, hipStream_t stream) {
+  if (dtype == 0)
+    return p.dm.D == 128 ? launch_split_first_t<0, 128, KV>(p, stream) : launch_split_first_t<0, 64, KV>(p, stream);
+  return p.dm.D == 128 ? launch_split_first_t<1, 128, KV>(p, stream) : launch_split_first_t<1, 64, KV>(p, stream);
+}
+
+// Requires p.chunk to be a multiple of 64 (sub-tiles start 64-aligned).
+hipError_t launch_paged_split_first(const SplitParams& p, int dtype, hipStream_t stream) {
+  return p.block_shift >= 6 ? launch_paged_t<1>(p, dtype, stream) : launch_paged_t<2>(p, dtype, stream);
 }
 
 hipError_t launch_split_reduce(const ReduceParams& p, int dtype, hipStream_t stream) {

@@ -17,9 +17,11 @@ DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 
 GQA_MAX_SPLITS = 1024
-ABI_VERSION = 2
+GQA_MAX_BLOCK_SIZE = 65536
+ABI_VERSION = 3
 
 _i64x4 = ctypes.c_int64 * 4
+_i64x3 = ctypes.c_int64 * 3
 _p = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
@@ -54,6 +56,15 @@ SIGNATURES = {
         _i,
         [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _p, _i,
          _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
+    "gqa_paged_split_first_launch": (
+        _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _i, _i, _p, _i,
+         _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
+    "gqa_paged_cache_write_launch": (
+        _i,
+        [_p, _i64x3, _p, _i64x3, _p, _i64x4, _p, _i64x4, _p, _i, _i, _i, _i, _i, _p],
     ),
 }
 
@@ -101,3 +112,8 @@ def check(code: int) -> None:
 def strides(t) -> "ctypes.Array":
     """The 4 element strides of a torch tensor as a C int64[4]."""
     return _i64x4(*t.stride())
+
+
+def strides3(t) -> "ctypes.Array":
+    """The 3 element strides of a 3-d torch tensor as a C int64[3]."""
+    return _i64x3(*t.stride())

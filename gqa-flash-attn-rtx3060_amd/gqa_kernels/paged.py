@@ -1,0 +1,423 @@
+"""Paged KV cache: attention over a block table, cache writes, prefix sharing.
+
+The reference lists a persistent prefix KV cache and a vLLM-shaped interface
+as the next step after its kernel (reference README.md:140-146: "Caching the
+K/V for the static prefix and computing attention only over the new tokens";
+"wrapping it in a vLLM-shaped Attention interface is mostly glue code"; "none
+of the above is in this repo").  This module is that step on MI355X:
+
+* ``paged_attention`` — the split-KV kernels of the contiguous decode path
+  reading K/V through a block table (libgqa_hip.so
+  ``gqa_paged_split_first_launch`` + ``gqa_split_reduce[_lse]_launch``), with
+  a length per sequence and the bottom-right causal alignment of
+  ``gqa_flash_attn`` applied per sequence.
+* ``write_kv`` — store new tokens' K/V at their cache slots
+  (``gqa_paged_cache_write_launch``).
+* ``PagedKVCache`` — host-side block allocator with reference-counted blocks:
+  a shared prefix (system prompt, memory block) is stored once and every
+  sequence forked from it attends to it without recomputing its K/V; a
+  partly filled shared block is copied before a sequence writes into it.
+* ``GQAPagedAttention`` / ``PagedAttentionMetadata`` — a vLLM-shaped layer:
+  ``forward(query, key, value, kv_cache, attn_metadata)`` on flattened
+  token-major tensors, cache ``(2, num_blocks, block_size, Hkv, D)``.
+
+Cache layout: ``k_cache``/``v_cache`` are ``(num_blocks, block_size, Hkv, D)``
+(block_size a power of two); key j of sequence b is slot ``j % block_size``
+of block ``block_table[b, j // block_size]``.  A slot index is
+``block * block_size + offset``.
+"""
+from __future__ import annotations
+
+import math
+import threading
+from dataclasses import dataclass
+from typing import Dict, Hashable, List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from .gqa_split import _workspace_buffer, workspace_bytes
+
+__all__ = [
+    "paged_attention",
+    "write_kv",
+    "paged_splits",
+    "PagedKVCache",
+    "PagedAttentionMetadata",
+    "GQAPagedAttention",
+]
+
+LOG2E = math.log2(math.e)
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
+
+# Split sizing, as for the contiguous decode route: one round of workgroups
+# at two per compute unit, chunks of at least two 128-key tiles.
+_SPLIT_ROWS = 32
+_SPLIT_WG_PER_CU = 2
+_MIN_CHUNK = 256
+
+_cu_lock = threading.Lock()
+_cu_counts: dict = {}
+
+
+def _cu_count(device_index: int) -> int:
+    with _cu_lock:
+        n = _cu_counts.get(device_index)
+        if n is None:
+            n = _lib.load().gqa_device_cu_count(device_index)
+            if n <= 0:
+                raise RuntimeError(f"gqa_device_cu_count({device_index}) failed: {n}")
+            _cu_counts[device_index] = n
+        return n
+
+
+def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
+                 cu_count: int) -> int:
+    """Split count for a paged call: the power of two that brings the first
+    pass to two workgroups per compute unit while every chunk keeps at least
+    256 keys (pure function of the shapes)."""
+    group = num_heads // num_kv_heads
+    base = -(-group * seq_q // _SPLIT_ROWS) * num_kv_heads * batch
+    target = _SPLIT_WG_PER_CU * cu_count
+    splits = 1
+    while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
+           and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
+        splits *= 2
+    return splits
+
+
+def _rows_ready(t: torch.Tensor) -> bool:
+    """Unit last-dim stride and 16-byte aligned rows (what the kernels load)."""
+    es = t.element_size()
+    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> int:
+    assert k_cache.dim() == 4 and tuple(k_cache.shape) == tuple(v_cache.shape), \
+        "k_cache / v_cache must be (num_blocks, block_size, num_kv_heads, head_dim)"
+    assert k_cache.dtype == v_cache.dtype and k_cache.device == v_cache.device
+    block_size = k_cache.shape[1]
+    assert 1 <= block_size <= _lib.GQA_MAX_BLOCK_SIZE and block_size & (block_size - 1) == 0, \
+        "block_size must be a power of two"
+    assert _rows_ready(k_cache) and _rows_ready(v_cache), "cache rows must be contiguous and 16-byte aligned"
+    return block_size
+
+
+def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
+                    max_seq_len: Optional[int] = None, scale: Optional[float] = None,
+                    splits: Optional[int] = None, return_lse: bool = False,
+                    out: Optional[torch.Tensor] = None):
+    """GQA attention of q over K/V held in a paged cache.
+
+    Args:
+        q: (batch, num_heads, seq_q, head_dim), fp16 or bf16 (any strides with
+            a contiguous, 16-byte aligned last dimension).
+        k_cache, v_cache: (num_blocks, block_size, num_kv_heads, head_dim),
+            q's dtype; block_size a power of two.
+        block_table: int32 (batch, max_blocks_per_seq); row b lists the
+            blocks of sequence b in key order (entries past the sequence's
+            length are not read).
+        seq_lens: int32 (batch,) — keys of each sequence, including the
+            seq_q new tokens (whose K/V must already be in the cache).
+        causal: query row i of sequence b attends keys
+            [0, i + seq_lens[b] - seq_q] (bottom-right alignment, as
+            gqa_flash_attn with seq_kv = seq_lens[b]).
+        max_seq_len: an upper bound of seq_lens (sizes the split chunks;
+            keys past it are not read).  Default: the table's capacity,
+            max_blocks_per_seq * block_size, which needs no device read.
+        scale: score scale (default head_dim ** -0.5, the reference's).
+        splits: split count (default: ``paged_splits``).
+        return_lse: also return the natural-log LSE per row, fp32
+            (batch, num_heads, seq_q).
+        out: optional (batch, num_heads, seq_q, head_dim) tensor of q's dtype
+            (any strides with 16-byte aligned rows) to write o into.
+
+    Returns:
+        o (batch, num_heads, seq_q, head_dim), or (o, lse).
+    """
+    batch, num_heads, seq_q, head_dim = q.shape
+    block_size = _check_cache(k_cache, v_cache)
+    num_kv_heads = k_cache.shape[2]
+    assert num_heads % num_kv_heads == 0, "num_heads must be divisible by num_kv_heads"
+    assert head_dim in (64, 128), f"unsupported head_dim {head_dim}"
+    assert k_cache.shape[3] == head_dim, "cache head_dim differs from q"
+    assert q.dtype in _DTYPES and k_cache.dtype == q.dtype, "q and the caches must share one fp16/bf16 dtype"
+    assert q.is_cuda and k_cache.device == q.device
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == batch
+    assert seq_lens.dtype == torch.int32 and tuple(seq_lens.shape) == (batch,)
+    assert block_table.device == q.device and seq_lens.device == q.device
+    if block_table.stride(1) != 1 or (batch > 1 and block_table.stride(0) < block_table.shape[1]):
+        block_table = block_table.contiguous()
+    seq_lens = seq_lens.contiguous()
+    if not _rows_ready(q):
+        q = q.contiguous()
+
+    table_stride = block_table.stride(0) if batch > 1 else block_table.shape[1]
+    capacity = block_table.shape[1] * block_size
+    if max_seq_len is None:
+        max_seq_len = capacity
+    assert 0 <= max_seq_len <= capacity, "max_seq_len exceeds the block table's capacity"
+    dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
+    if splits is None:
+        splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev))
+    if scale is None:
+        scale = head_dim ** -0.5
+
+    if out is None:
+        out = torch.empty(batch, num_heads, seq_q, head_dim, dtype=q.dtype, device=q.device)
+    else:
+        assert tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype and out.device == q.device
+        assert _rows_ready(out), "out rows must be contiguous and 16-byte aligned"
+
+    lib = _lib.load()
+    dtype = _DTYPES[q.dtype]
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    workspace = _workspace_buffer(q.device, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, splits))
+    _lib.check(lib.gqa_paged_split_first_launch(
+        q.data_ptr(), _lib.strides(q), k_cache.data_ptr(), _lib.strides(k_cache),
+        v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
+        seq_lens.data_ptr(), block_size, max_seq_len, workspace.data_ptr(), splits,
+        batch, num_heads, num_kv_heads, seq_q, head_dim, scale * LOG2E, int(bool(causal)), dtype, stream))
+    if not return_lse:
+        _lib.check(lib.gqa_split_reduce_launch(workspace.data_ptr(), splits, out.data_ptr(), _lib.strides(out),
+                                               batch, num_heads, seq_q, head_dim, dtype, stream))
+        return out
+    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device)
+    _lib.check(lib.gqa_split_reduce_lse_launch(workspace.data_ptr(), splits, out.data_ptr(), _lib.strides(out),
+                                               lse.data_ptr(), batch, num_heads, seq_q, head_dim, dtype, stream))
+    return out, lse
+
+
+def write_kv(key, value, k_cache, v_cache, slot_mapping):
+    """Store K/V of new tokens at their cache slots (in place).
+
+    key, value: (num_tokens, num_kv_heads, head_dim) in the caches' dtype;
+    slot_mapping: int64 (num_tokens,), slot = block * block_size + offset,
+    negative = skip (padding).  Every non-negative slot must lie inside the
+    caches.
+    """
+    block_size = _check_cache(k_cache, v_cache)
+    num_tokens, num_kv_heads, head_dim = key.shape
+    assert tuple(value.shape) == tuple(key.shape)
+    assert k_cache.shape[2] == num_kv_heads and k_cache.shape[3] == head_dim
+    assert key.dtype == k_cache.dtype == value.dtype and key.dtype in _DTYPES
+    assert slot_mapping.dtype == torch.int64 and tuple(slot_mapping.shape) == (num_tokens,)
+    assert key.device == value.device == k_cache.device == slot_mapping.device and key.is_cuda
+    slot_mapping = slot_mapping.contiguous()
+    key = key if _rows_ready(key) else key.contiguous()
+    value = value if _rows_ready(value) else value.contiguous()
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(key.device).cuda_stream
+    _lib.check(lib.gqa_paged_cache_write_launch(
+        key.data_ptr(), _lib.strides3(key), value.data_ptr(), _lib.strides3(value),
+        k_cache.data_ptr(), _lib.strides(k_cache), v_cache.data_ptr(), _lib.strides(v_cache),
+        slot_mapping.data_ptr(), num_tokens, num_kv_heads, head_dim, block_size, _DTYPES[key.dtype], stream))
+
+
+# ---------------------------------------------------------------------------
+# Block allocator with prefix sharing
+# ---------------------------------------------------------------------------
+class _Seq:
+    __slots__ = ("blocks", "length")
+
+    def __init__(self, blocks: List[int], length: int):
+        self.blocks = blocks
+        self.length = length
+
+
+class PagedKVCache:
+    """K/V of many sequences in one pair of paged caches.
+
+    Blocks are reference counted: ``fork`` gives a new sequence the blocks of
+    an existing one (a persistent prefix is computed and stored once), and a
+    partly filled block that more than one sequence holds is copied before
+    one of them appends to it, so forks never see each other's new tokens.
+
+    The K/V tensors are ``kv[0]`` and ``kv[1]`` of one
+    ``(2, num_blocks, block_size, num_kv_heads, head_dim)`` tensor, the
+    layout a vLLM attention backend receives as ``kv_cache``.
+    """
+
+    def __init__(self, num_blocks: int, block_size: int, num_kv_heads: int, head_dim: int,
+                 dtype=torch.bfloat16, device="cuda"):
+        assert num_blocks > 0 and block_size > 0 and block_size & (block_size - 1) == 0
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.kv = torch.zeros(2, num_blocks, block_size, num_kv_heads, head_dim, dtype=dtype, device=device)
+        self._free: List[int] = list(range(num_blocks - 1, -1, -1))
+        self._refs: List[int] = [0] * num_blocks
+        self._seqs: Dict[Hashable, _Seq] = {}
+
+    # -- views ---------------------------------------------------------------
+    @property
+    def k_cache(self) -> torch.Tensor:
+        return self.kv[0]
+
+    @property
+    def v_cache(self) -> torch.Tensor:
+        return self.kv[1]
+
+    def num_free_blocks(self) -> int:
+        return len(self._free)
+
+    def seq_len(self, seq_id) -> int:
+        return self._seqs[seq_id].length
+
+    def blocks(self, seq_id) -> List[int]:
+        return list(self._seqs[seq_id].blocks)
+
+    # -- sequence lifetime ---------------------------------------------------
+    def add_sequence(self, seq_id) -> None:
+        assert seq_id not in self._seqs, f"sequence {seq_id!r} exists"
+        self._seqs[seq_id] = _Seq([], 0)
+
+    def fork(self, src_id, dst_id) -> None:
+        """New sequence dst_id sharing every block (and the length) of src_id."""
+        assert dst_id not in self._seqs, f"sequence {dst_id!r} exists"
+        src = self._seqs[src_id]
+        for b in src.blocks:
+            self._refs[b] += 1
+        self._seqs[dst_id] = _Seq(list(src.blocks), src.length)
+
+    def free(self, seq_id) -> None:
+        for b in self._seqs.pop(seq_id).blocks:
+            self._refs[b] -= 1
+            if self._refs[b] == 0:
+                self._free.append(b)
+
+    def _alloc(self) -> int:
+        if not self._free:
+            raise RuntimeError("paged KV cache out of blocks")
+        b = self._free.pop()
+        self._refs[b] = 1
+        return b
+
+    # -- writing -------------------------------------------------------------
+    def reserve(self, seq_id, n: int) -> List[int]:
+        """Slots for the next n tokens of seq_id (allocating blocks, copying a
+        shared partly filled last block first); the length grows by n."""
+        s = self._seqs[seq_id]
+        bs = self.block_size
+        if n <= 0:
+            return []
+        cow = s.length % bs != 0 and self._refs[s.blocks[-1]] > 1
+        need = -(-(s.length + n) // bs) - len(s.blocks)
+        if need + cow > len(self._free):
+            raise RuntimeError("paged KV cache out of blocks")
+        if cow:
+            old = s.blocks[-1]
+            new = self._alloc()
+            self.kv[:, new].copy_(self.kv[:, old])
+            self._refs[old] -= 1
+            s.blocks[-1] = new
+        for _ in range(need):
+            s.blocks.append(self._alloc())
+        slots = [s.blocks[j // bs] * bs + j % bs for j in range(s.length, s.length + n)]
+        s.length += n
+        return slots
+
+    def append(self, seq_ids: Sequence, key: torch.Tensor, value: torch.Tensor,
+               num_new: Optional[Sequence[int]] = None) -> torch.Tensor:
+        """Append K/V of new tokens, sequence-major: the first num_new[0]
+        rows of key/value (num_tokens, num_kv_heads, head_dim) belong to
+        seq_ids[0], and so on (default: an equal share each).  Returns the
+        int64 slot mapping written."""
+        if num_new is None:
+            assert key.shape[0] % len(seq_ids) == 0
+            num_new = [key.shape[0] // len(seq_ids)] * len(seq_ids)
+        assert sum(num_new) == key.shape[0]
+        slots: List[int] = []
+        for sid, n in zip(seq_ids, num_new):
+            slots += self.reserve(sid, n)
+        slot_mapping = torch.tensor(slots, dtype=torch.int64).to(self.kv.device)
+        write_kv(key, value, self.k_cache, self.v_cache, slot_mapping)
+        return slot_mapping
+
+    # -- attention -----------------------------------------------------------
+    def block_table(self, seq_ids: Sequence) -> torch.Tensor:
+        """int32 (len(seq_ids), max blocks) on the cache's device; unused
+        entries are 0 (never read)."""
+        rows = [self._seqs[s].blocks for s in seq_ids]
+        width = max(1, max(len(r) for r in rows))
+        table = torch.zeros(len(rows), width, dtype=torch.int32)
+        for i, r in enumerate(rows):
+            if r:
+                table[i, :len(r)] = torch.tensor(r, dtype=torch.int32)
+        return table.to(self.kv.device)
+
+    def seq_lens(self, seq_ids: Sequence) -> torch.Tensor:
+        return torch.tensor([self._seqs[s].length for s in seq_ids], dtype=torch.int32).to(self.kv.device)
+
+    def attend(self, q: torch.Tensor, seq_ids: Sequence, causal: bool = True, *, return_lse: bool = False):
+        """paged_attention of q (len(seq_ids), num_heads, seq_q, head_dim)
+        over these sequences (their new tokens already appended)."""
+        max_len = max(self._seqs[s].length for s in seq_ids)
+        return paged_attention(q, self.k_cache, self.v_cache, self.block_table(seq_ids), self.seq_lens(seq_ids),
+                               causal, max_seq_len=max_len, return_lse=return_lse)
+
+
+# ---------------------------------------------------------------------------
+# vLLM-shaped layer
+# ---------------------------------------------------------------------------
+@dataclass
+class PagedAttentionMetadata:
+    """Per-step batch description, in the names vLLM's attention metadata uses.
+
+    slot_mapping: int64 (num_tokens,) cache slot of every new token (-1: pad).
+    block_tables: int32 (num_seqs, max_blocks_per_seq).
+    seq_lens: int32 (num_seqs,) keys per sequence, new tokens included.
+    query_len: new tokens per sequence (the same for every sequence: 1 for
+        decode, k for speculative verification, the chunk for chunked prefill).
+    max_seq_len: an upper bound of seq_lens (default: the tables' capacity).
+    """
+    slot_mapping: torch.Tensor
+    block_tables: torch.Tensor
+    seq_lens: torch.Tensor
+    query_len: int = 1
+    max_seq_len: Optional[int] = None
+
+
+class GQAPagedAttention(torch.nn.Module):
+    """Attention layer with the call shape of a vLLM attention backend.
+
+    ``forward(query, key, value, kv_cache, attn_metadata)``:
+      query (num_tokens, num_heads * head_size), key/value
+      (num_tokens, num_kv_heads * head_size) or None (nothing to store),
+      kv_cache (2, num_blocks, block_size, num_kv_heads, head_size).
+    Tokens are sequence-major, ``attn_metadata.query_len`` per sequence.  The
+    new K/V are stored at ``slot_mapping`` first, then every query attends its
+    sequence's cache (causal, bottom-right aligned).  Returns
+    (num_tokens, num_heads * head_size), written in place when ``output`` is
+    given.
+    """
+
+    def __init__(self, num_heads: int, head_size: int, scale: Optional[float] = None,
+                 num_kv_heads: Optional[int] = None, causal: bool = True):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.num_kv_heads = num_heads if num_kv_heads is None else num_kv_heads
+        assert num_heads % self.num_kv_heads == 0, "num_heads must be divisible by num_kv_heads"
+        assert head_size in (64, 128), f"unsupported head_size {head_size}"
+        self.scale = head_size ** -0.5 if scale is None else float(scale)
+        self.causal = causal
+
+    def forward(self, query, key, value, kv_cache, attn_metadata: PagedAttentionMetadata, output=None):
+        md = attn_metadata
+        num_tokens = query.shape[0]
+        H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_size
+        sq = md.query_len
+        batch = md.block_tables.shape[0]
+        assert num_tokens == batch * sq, "num_tokens must equal num_seqs * query_len"
+        assert kv_cache.dim() == 5 and kv_cache.shape[0] == 2 and kv_cache.shape[3] == Hkv and kv_cache.shape[4] == D
+        k_cache, v_cache = kv_cache[0], kv_cache[1]
+        if key is not None:
+            write_kv(key.view(num_tokens, Hkv, D), value.view(num_tokens, Hkv, D), k_cache, v_cache,
+                     md.slot_mapping)
+        if output is None:
+            output = torch.empty(num_tokens, H * D, dtype=query.dtype, device=query.device)
+        q4 = query.view(batch, sq, H, D).permute(0, 2, 1, 3)
+        o4 = output.view(batch, sq, H, D).permute(0, 2, 1, 3)
+        paged_attention(q4, k_cache, v_cache, md.block_tables, md.seq_lens, self.causal,
+                        max_seq_len=md.max_seq_len, scale=self.scale, out=o4)
+        return output

@@ -46,8 +46,11 @@ extern "C" {
 #define GQA_E_SPLITS (-5)     /* splits outside [1, GQA_MAX_SPLITS] */
 #define GQA_E_GROUP (-6)      /* group size above what one packed tile holds */
 #define GQA_E_NULL (-7)       /* null pointer argument */
+#define GQA_E_BLOCK (-8)      /* paged cache: block_size not a power of two in
+                                 [1, GQA_MAX_BLOCK_SIZE], or table too short */
 
 #define GQA_MAX_SPLITS 1024
+#define GQA_MAX_BLOCK_SIZE 65536
 
 /* ABI revision; bumped when a signature below changes. */
 int gqa_abi_version(void);
@@ -157,6 +160,52 @@ int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4],
                                int seq_q, int seq_kv, int head_dim,
                                float scale_log2, int causal, int dtype,
                                void* stream);
+
+/* Paged KV cache.  The reference names a persistent prefix KV cache and a
+ * vLLM-shaped interface as the next step after its kernel (README.md:140-146,
+ * "none of the above is in this repo"); these entry points are that step.
+ * K and V of all sequences live in caches of shape
+ *   k_cache, v_cache : (num_blocks, block_size, num_kv_heads, head_dim)
+ * (element strides in that order, last one 1, rows 16-byte aligned), with
+ * block_size a power of two.  Key j of sequence b is slot j % block_size of
+ * block block_table[b * table_stride + j / block_size]; sequence b has
+ * seq_lens[b] keys.  block_table and seq_lens are int32 device arrays.
+ * Sequences may share blocks (a common prefix stored once). */
+
+/* Split-KV first pass over a paged cache; combine with
+ * gqa_split_reduce_launch / gqa_split_reduce_lse_launch (same workspace
+ * layout).  q is (batch, num_heads, seq_q, head_dim) as above; with causal,
+ * query row i of sequence b attends keys [0, i + seq_lens[b] - seq_q]
+ * (the bottom-right alignment of the contiguous path, per sequence).
+ * max_seq_len bounds the sequences (seq_lens[b] is clamped to
+ * [0, max_seq_len]; keys past it are not read) and sets the chunk size: chunk s covers keys
+ * [s*C, (s+1)*C) with C = ceil(max_seq_len / splits) rounded up to a
+ * multiple of 64.  Every table entry a sequence reaches must index a block
+ * of the caches; table_stride * block_size >= max_seq_len. */
+int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4],
+                                 const void* k_cache, const int64_t k_cache_stride[4],
+                                 const void* v_cache, const int64_t v_cache_stride[4],
+                                 const int* block_table, int table_stride,
+                                 const int* seq_lens, int block_size, int max_seq_len,
+                                 float* workspace, int splits,
+                                 int batch, int num_heads, int num_kv_heads,
+                                 int seq_q, int head_dim,
+                                 float scale_log2, int causal, int dtype,
+                                 void* stream);
+
+/* Store new tokens' K and V into the paged caches:
+ * k_cache[slot / block_size, slot % block_size, h, :] = k[t, h, :] (and V)
+ * with slot = slot_mapping[t] (int64); tokens whose slot is negative are
+ * skipped (padding).  k, v : (num_tokens, num_kv_heads, head_dim) with
+ * element strides k_stride / v_stride (last one 1, rows 16-byte aligned).
+ * Every non-negative slot must lie inside the caches. */
+int gqa_paged_cache_write_launch(const void* k, const int64_t k_stride[3],
+                                 const void* v, const int64_t v_stride[3],
+                                 void* k_cache, const int64_t k_cache_stride[4],
+                                 void* v_cache, const int64_t v_cache_stride[4],
+                                 const int64_t* slot_mapping, int num_tokens,
+                                 int num_kv_heads, int head_dim, int block_size,
+                                 int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,11 @@ values, which for bf16/fp16 inputs are the bf16/fp16-rounded numbers):
   gqa_split.py:134-139, without returning it); -inf for a row with no visible
   key.  ``split_lse`` forms it from split partials the way that combine does.
 
+* ``paged_gather`` / ``paged_reference`` — a paged K/V cache (the
+  reference's roadmap item, README.md:140-146; not in the reference) read
+  back into contiguous per-sequence K/V, and ``gqa_reference`` / ``gqa_lse``
+  per sequence over it.
+
 Parity pinning (tests/test_oracle.py): brute-force scalar loops at tiny
 shapes, closed forms (one-key row, constant V, constant-per-head V, uniform
 keys), invariants (chunked = last rows of prefill, decode causal = non-causal,
@@ -46,7 +51,8 @@ import math
 import numpy as np
 
 __all__ = ["gqa_reference", "gqa_lse", "split_partials", "split_combine", "split_kv_reference",
-           "split_lse", "attention_flops", "attention_bytes", "visible_pairs"]
+           "split_lse", "paged_gather", "paged_reference", "attention_flops", "attention_bytes",
+           "visible_pairs"]
 
 LOG2E = math.log2(math.e)
 
@@ -186,6 +192,43 @@ def split_lse(m, l):
 def split_kv_reference(q, k, v, causal, splits, *, dtype=np.float64):
     """Split-KV forward on the CPU (first pass + combine)."""
     return split_combine(*split_partials(q, k, v, causal, splits, dtype=dtype))
+
+
+def paged_gather(k_cache, v_cache, block_table, seq_lens):
+    """K and V of each sequence of a paged cache as contiguous arrays.
+
+    k_cache, v_cache: (num_blocks, block_size, Hkv, D); block_table
+    (B, max_blocks) and seq_lens (B,) integer arrays.  Key j of sequence b is
+    slot j % block_size of block block_table[b, j // block_size] (the layout
+    the paged entry points read; the reference has no paged cache, its
+    roadmap names one at README.md:140-146).  Returns a list of B pairs of
+    (1, Hkv, seq_lens[b], D) arrays, the (batch, kv head, key, d) order of
+    reference gqa_kernels/dispatch.py:17-27 with batch 1.
+    """
+    k_cache = np.asarray(k_cache)
+    v_cache = np.asarray(v_cache)
+    table = np.asarray(block_table, dtype=np.int64)
+    bs = k_cache.shape[1]
+    out = []
+    for b, n in enumerate(np.asarray(seq_lens, dtype=np.int64)):
+        j = np.arange(int(n))
+        blk, off = table[b, j // bs], j % bs
+        out.append((k_cache[blk, off].transpose(1, 0, 2)[None], v_cache[blk, off].transpose(1, 0, 2)[None]))
+    return out
+
+
+def paged_reference(q, k_cache, v_cache, block_table, seq_lens, causal=True, *, dtype=np.float64):
+    """Attention of q (B, Hq, Sq, D) over a paged cache: for each sequence b,
+    ``gqa_reference`` of q[b] against its gathered keys (seq_kv = seq_lens[b],
+    so the causal alignment is bottom-right per sequence).  Returns
+    (o (B, Hq, Sq, D), lse (B, Hq, Sq))."""
+    q = np.asarray(q)
+    o = np.empty(q.shape, dtype=dtype)
+    lse = np.empty(q.shape[:3], dtype=np.float64)
+    for b, (kb, vb) in enumerate(paged_gather(k_cache, v_cache, block_table, seq_lens)):
+        o[b] = gqa_reference(q[b:b + 1], kb, vb, causal, dtype=dtype)[0]
+        lse[b] = gqa_lse(q[b:b + 1], kb, vb, causal)[0]
+    return o, lse
 
 
 def visible_pairs(seq_q: int, seq_kv: int, causal: bool) -> int:

@@ -1,0 +1,223 @@
+"""GPU parity of the paged KV-cache path (paged_attention, write_kv,
+PagedKVCache, GQAPagedAttention) against the CPU oracle's paged_reference
+(per-sequence gqa_reference over the gathered K/V), at the bf16/fp16 gates of
+the contiguous path; the cache write is checked bit-exactly."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BASELINE_TOL, assert_close, to_np
+from oracle.gqa_oracle import paged_reference
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+LSE_TOL = 2e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+def _paged_inputs(B, Hq, Hkv, Sq, lens, D, block_size, dtype, seed, spare_blocks=5, width_pad=2):
+    """Random q and a paged cache holding `lens[b]` keys per sequence at a
+    shuffled block assignment (unused blocks and table entries hold junk that
+    must never be read: NaN in the cache, 0 in the table)."""
+    g = torch.Generator().manual_seed(seed)
+    per = [-(-n // block_size) for n in lens]
+    nblk = sum(per) + spare_blocks
+    kc = torch.full((nblk, block_size, Hkv, D), float("nan"))
+    vc = torch.full((nblk, block_size, Hkv, D), float("nan"))
+    perm = torch.randperm(nblk, generator=g).tolist()
+    table = torch.zeros(B, max(per) + width_pad, dtype=torch.int32)
+    for b, n in enumerate(lens):
+        blocks = [perm.pop() for _ in range(per[b])]
+        table[b, :len(blocks)] = torch.tensor(blocks, dtype=torch.int32)
+        if n:
+            k = torch.randn(n, Hkv, D, generator=g)
+            v = torch.randn(n, Hkv, D, generator=g)
+            j = torch.arange(n)
+            kc[table[b, j // block_size].long(), j % block_size] = k
+            vc[table[b, j // block_size].long(), j % block_size] = v
+    q = torch.randn(B, Hq, Sq, D, generator=g)
+    q, kc, vc = (t.to(dtype) for t in (q, kc, vc))
+    seq_lens = torch.tensor(lens, dtype=torch.int32)
+    return q, kc, vc, table, seq_lens
+
+
+def _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype):
+    ref_o, ref_lse = paged_reference(to_np(q), to_np(kc), to_np(vc), table.numpy(), seq_lens.numpy(), causal)
+    got = to_np(o)
+    nan = np.isnan(ref_o)
+    assert np.array_equal(np.isnan(got), nan), "fully masked rows differ"
+    assert_close(got[~nan], ref_o[~nan], BASELINE_TOL[dtype], "paged")
+    if lse is not None:
+        got_l = to_np(lse).astype(np.float64)
+        fin = np.isfinite(ref_lse)
+        assert np.array_equal(np.isneginf(got_l), ~fin)
+        assert np.abs(got_l[fin] - ref_lse[fin]).max() <= LSE_TOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,lens,D,bs,dtype,causal", [
+    (4, 32, 8, 1, [1, 77, 300, 1024], 128, 16, torch.bfloat16, True),     # small pages, ragged
+    (4, 32, 8, 1, [2000, 64, 129, 700], 128, 64, torch.bfloat16, True),   # 64-key pages
+    (2, 32, 8, 1, [5000, 3001], 128, 128, torch.float16, True),           # 128-key pages, fp16
+    (3, 64, 8, 4, [4096, 10, 555], 128, 32, torch.bfloat16, True),        # G=8, 4-token verify
+    (2, 32, 8, 3, [2, 900], 64, 8, torch.float16, True),                  # seq shorter than Sq: masked rows
+    (2, 32, 4, 16, [1500, 260], 64, 256, torch.bfloat16, False),          # chunk, non-causal, big pages
+    (1, 16, 16, 1, [333], 128, 1, torch.bfloat16, True),                  # MHA, one-slot pages
+])
+def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal):
+    from gqa_kernels.paged import paged_attention
+    q, kc, vc, table, seq_lens = _paged_inputs(B, Hq, Hkv, Sq, lens, D, bs, dtype, seed=sum(lens))
+    print(f"paged B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} lens={lens} D={D} bs={bs} {dtype}", flush=True)
+    args = (q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), causal)
+    o, lse = paged_attention(*args, max_seq_len=max(lens), return_lse=True)
+    o2 = paged_attention(*args)  # default bound: the table's capacity (more, empty splits)
+    torch.cuda.synchronize()
+    _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype)
+    _check(o2, None, q, kc, vc, table, seq_lens, causal, dtype)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 16])
+def test_paged_split_counts(splits):
+    from gqa_kernels.paged import paged_attention
+    q, kc, vc, table, seq_lens = _paged_inputs(2, 32, 8, 1, [3000, 1200], 128, 64, torch.bfloat16, seed=7)
+    o = paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), True,
+                        max_seq_len=3000, splits=splits)
+    torch.cuda.synchronize()
+    _check(o, None, q, kc, vc, table, seq_lens, True, torch.bfloat16)
+
+
+def test_paged_equals_contiguous_at_decode_scale():
+    """131072 keys in 128-key pages (shuffled) vs the contiguous split-KV
+    route on the same K/V: same math, different chunking."""
+    from gqa_kernels import gqa_flash_attn
+    from gqa_kernels.paged import paged_attention
+    Hq, Hkv, L, D, bs = 32, 8, 131072, 128, 128
+    g = torch.Generator(device=DEV).manual_seed(11)
+    k = torch.randn(1, Hkv, L, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(1, Hkv, L, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(1, Hq, 1, D, generator=g, device=DEV).to(torch.bfloat16)
+    nblk = L // bs
+    perm = torch.randperm(nblk, generator=g, device=DEV)
+    kc = torch.empty(nblk, bs, Hkv, D, dtype=torch.bfloat16, device=DEV)
+    vc = torch.empty_like(kc)
+    kc[perm] = k[0].permute(1, 0, 2).reshape(nblk, bs, Hkv, D)
+    vc[perm] = v[0].permute(1, 0, 2).reshape(nblk, bs, Hkv, D)
+    table = perm.to(torch.int32)[None]
+    o_p = paged_attention(q, kc, vc, table, torch.tensor([L], dtype=torch.int32, device=DEV), True)
+    o_c = gqa_flash_attn(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert_close(o_p, o_c, BASELINE_TOL[torch.bfloat16], "paged vs contiguous")
+
+
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16)])
+def test_write_kv_is_exact(D, dtype):
+    from gqa_kernels.paged import write_kv
+    nblk, bs, Hkv, T = 20, 16, 8, 57
+    g = torch.Generator().manual_seed(2)
+    kc = torch.randn(nblk, bs, Hkv, D, generator=g).to(dtype)
+    vc = torch.randn(nblk, bs, Hkv, D, generator=g).to(dtype)
+    key = torch.randn(T, Hkv, D, generator=g).to(dtype)
+    val = torch.randn(T, Hkv, D, generator=g).to(dtype)
+    slots = torch.randperm(nblk * bs, generator=g)[:T]
+    slots[::7] = -1  # padding tokens are skipped
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    # key/value as strided views of a wider (T, 2*Hkv*D) projection output
+    kv = torch.cat([key.reshape(T, -1), val.reshape(T, -1)], dim=1).to(DEV)
+    write_kv(kv[:, :Hkv * D].view(T, Hkv, D), kv[:, Hkv * D:].view(T, Hkv, D), kc_d, vc_d, slots.to(DEV))
+    torch.cuda.synchronize()
+    keep = slots >= 0
+    kc[slots[keep] // bs, slots[keep] % bs] = key[keep]
+    vc[slots[keep] // bs, slots[keep] % bs] = val[keep]
+    assert torch.equal(kc_d.cpu(), kc) and torch.equal(vc_d.cpu(), vc)
+
+
+def test_prefix_cache_shared_across_sequences():
+    """A 1000-token prefix stored once; three forks append their own turns
+    (a chunk, then decode steps) and attend over prefix + own tokens."""
+    from gqa_kernels.paged import PagedKVCache
+    Hq, Hkv, D, bs = 32, 8, 128, 64
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(9)
+    cache = PagedKVCache(200, bs, Hkv, D, dtype=dt, device=DEV)
+    kp = torch.randn(1000, Hkv, D, generator=g).to(dt)
+    vp = torch.randn(1000, Hkv, D, generator=g).to(dt)
+    cache.add_sequence("prefix")
+    cache.append(["prefix"], kp.to(DEV), vp.to(DEV))
+    used = cache.num_blocks - cache.num_free_blocks()
+    keys = {s: [kp] for s in "abc"}
+    vals = {s: [vp] for s in "abc"}
+    for s in "abc":
+        cache.fork("prefix", s)
+    # turn: 24-token chunk per fork (batched), then 3 decode steps
+    for step, n in enumerate([24, 1, 1, 1]):
+        kn = torch.randn(3 * n, Hkv, D, generator=g).to(dt)
+        vn = torch.randn(3 * n, Hkv, D, generator=g).to(dt)
+        q = torch.randn(3, Hq, n, D, generator=g).to(dt)
+        cache.append(list("abc"), kn.to(DEV), vn.to(DEV))
+        for i, s in enumerate("abc"):
+            keys[s].append(kn[i * n:(i + 1) * n])
+            vals[s].append(vn[i * n:(i + 1) * n])
+        o, lse = cache.attend(q.to(DEV), list("abc"), return_lse=True)
+        torch.cuda.synchronize()
+        # oracle: contiguous prefix + own tokens per sequence, as a 1-block-per-key table
+        for i, s in enumerate("abc"):
+            k_all = torch.cat(keys[s])
+            v_all = torch.cat(vals[s])
+            L = k_all.shape[0]
+            ref_o, ref_l = paged_reference(to_np(q[i:i + 1]), to_np(k_all[:, None]), to_np(v_all[:, None]),
+                                           np.arange(L)[None], np.array([L]), True)
+            assert_close(to_np(o[i:i + 1]), ref_o, BASELINE_TOL[dt], f"fork {s} step {step}")
+            assert np.abs(to_np(lse[i:i + 1]) - ref_l).max() <= LSE_TOL
+    # the prefix's 15 full blocks are stored once; its partial 16th was copied per fork
+    assert cache.blocks("a")[:15] == cache.blocks("prefix")[:15] == cache.blocks("b")[:15]
+    assert len({cache.blocks(s)[15] for s in ("prefix", "a", "b", "c")}) == 4
+    # plus one copied block and one new block per fork
+    assert cache.num_blocks - cache.num_free_blocks() == used + 6
+
+
+def test_vllm_shaped_layer_decode_and_chunk():
+    from gqa_kernels.paged import GQAPagedAttention, PagedAttentionMetadata, PagedKVCache
+    Hq, Hkv, D, bs = 32, 8, 128, 16
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(13)
+    cache = PagedKVCache(400, bs, Hkv, D, dtype=dt, device=DEV)
+    layer = GQAPagedAttention(Hq, D, scale=0.05, num_kv_heads=Hkv)
+    hist = {}
+    lens0 = [700, 33, 1500]
+    for s, n in enumerate(lens0):
+        cache.add_sequence(s)
+        k = torch.randn(n, Hkv, D, generator=g).to(dt)
+        v = torch.randn(n, Hkv, D, generator=g).to(dt)
+        cache.append([s], k.to(DEV), v.to(DEV))
+        hist[s] = (k, v)
+    for sq in (1, 5):
+        B = 3
+        query = torch.randn(B * sq, Hq * D, generator=g).to(dt)
+        key = torch.randn(B * sq, Hkv * D, generator=g).to(dt)
+        value = torch.randn(B * sq, Hkv * D, generator=g).to(dt)
+        slots = torch.tensor(sum((cache.reserve(s, sq) for s in range(B)), []), dtype=torch.int64)
+        md = PagedAttentionMetadata(slot_mapping=slots.to(DEV), block_tables=cache.block_table(range(B)),
+                                    seq_lens=cache.seq_lens(range(B)), query_len=sq)
+        out = layer(query.to(DEV), key.to(DEV), value.to(DEV), cache.kv, md)
+        torch.cuda.synchronize()
+        assert tuple(out.shape) == (B * sq, Hq * D)
+        for s in range(B):
+            k, v = hist[s]
+            k = torch.cat([k, key[s * sq:(s + 1) * sq].view(sq, Hkv, D)])
+            v = torch.cat([v, value[s * sq:(s + 1) * sq].view(sq, Hkv, D)])
+            hist[s] = (k, v)
+            L = k.shape[0]
+            # scale 0.05 = D^-0.5 applied to q * (0.05 * sqrt(D))
+            q4 = to_np(query[s * sq:(s + 1) * sq].view(sq, Hq, D).permute(1, 0, 2)[None]).astype(np.float64)
+            q4 = q4 * (0.05 * D ** 0.5)
+            ref_o, _ = paged_reference(q4, to_np(k[:, None]), to_np(v[:, None]), np.arange(L)[None],
+                                       np.array([L]), True)
+            got = to_np(out[s * sq:(s + 1) * sq].view(sq, Hq, D).permute(1, 0, 2)[None])
+            assert_close(got, ref_o, BASELINE_TOL[dt], f"layer seq {s} sq {sq}")

@@ -1,0 +1,254 @@
+"""Paged KV cache, CPU side: the oracle's gather against an independent
+scatter, the C-ABI validation of the paged entry points (no kernel runs:
+every call here is rejected before any HIP call, or is an empty no-op), the
+split sizing, and the host block allocator (prefix sharing, copy on write,
+reference counts) on CPU tensors."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.gqa_oracle import gqa_lse, gqa_reference, paged_gather, paged_reference
+
+
+# ---------------------------------------------------------------------------
+# Oracle pins
+# ---------------------------------------------------------------------------
+def _scatter_loops(k, v, lens, block_size, num_blocks, rng):
+    """Write contiguous per-sequence K/V (B, Hkv, L, D) into a paged cache by
+    scalar loops, at a random block assignment; returns cache + table."""
+    B, Hkv, L, D = k.shape
+    kc = np.full((num_blocks, block_size, Hkv, D), np.nan)
+    vc = np.full((num_blocks, block_size, Hkv, D), np.nan)
+    free = list(rng.permutation(num_blocks))
+    width = max(-(-n // block_size) for n in lens)
+    table = np.zeros((B, width), dtype=np.int32)
+    for b in range(B):
+        for i in range(-(-lens[b] // block_size)):
+            table[b, i] = free.pop()
+        for j in range(lens[b]):
+            for h in range(Hkv):
+                kc[table[b, j // block_size], j % block_size, h] = k[b, h, j]
+                vc[table[b, j // block_size], j % block_size, h] = v[b, h, j]
+    return kc, vc, table
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 16])
+def test_paged_gather_inverts_scatter(block_size):
+    rng = np.random.default_rng(3)
+    B, Hkv, L, D = 3, 2, 37, 8
+    k = rng.standard_normal((B, Hkv, L, D))
+    v = rng.standard_normal((B, Hkv, L, D))
+    lens = [37, 1, 20]
+    kc, vc, table = _scatter_loops(k, v, lens, block_size, 64, rng)
+    got = paged_gather(kc, vc, table, lens)
+    for b in range(B):
+        assert np.array_equal(got[b][0][0], k[b, :, :lens[b]])
+        assert np.array_equal(got[b][1][0], v[b, :, :lens[b]])
+    # planted mistake: a gather that skips the block table (block j // bs)
+    j = np.arange(lens[0])
+    assert not np.array_equal(kc[j // block_size, j % block_size].transpose(1, 0, 2), k[0])
+
+
+def test_paged_reference_is_per_sequence_attention():
+    rng = np.random.default_rng(4)
+    B, Hq, Hkv, Sq, L, D = 3, 8, 2, 3, 50, 16
+    q = rng.standard_normal((B, Hq, Sq, D))
+    k = rng.standard_normal((B, Hkv, L, D))
+    v = rng.standard_normal((B, Hkv, L, D))
+    lens = [50, 2, 33]  # sequence 1 is shorter than Sq: its first row sees no key
+    kc, vc, table = _scatter_loops(k, v, lens, 8, 40, rng)
+    for causal in (True, False):
+        o, lse = paged_reference(q, kc, vc, table, lens, causal)
+        for b in range(B):
+            ref = gqa_reference(q[b:b + 1], k[b:b + 1, :, :lens[b]], v[b:b + 1, :, :lens[b]], causal,
+                                dtype=np.float64)
+            np.testing.assert_array_equal(o[b:b + 1], ref)
+            np.testing.assert_array_equal(lse[b:b + 1], gqa_lse(q[b:b + 1], k[b:b + 1, :, :lens[b]],
+                                                                 v[b:b + 1, :, :lens[b]], causal))
+        # per-sequence bottom-right alignment: row 0 of sequence 1 (2 keys, 3 queries) sees nothing
+        if causal:
+            assert np.isnan(o[1, :, 0]).all() and np.isneginf(lse[1, :, 0]).all()
+            assert np.isfinite(o[1, :, 1:]).all()
+
+
+# ---------------------------------------------------------------------------
+# C-ABI validation
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def lib():
+    from gqa_kernels import _lib
+    return _lib.load()
+
+
+_S4 = (ctypes.c_int64 * 4)(8 * 128 * 128, 128 * 128, 128, 1)
+_C4 = (ctypes.c_int64 * 4)(64 * 8 * 128, 8 * 128, 128, 1)  # (blocks, 64 slots, 8 heads, 128)
+_FAKE = ctypes.c_void_p(1 << 20)
+
+
+def _paged(lib, **kw):
+    a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16,
+             lens=_FAKE, bs=64, max_len=1024, ws=_FAKE, splits=8, B=2, Hq=32, Hkv=8, Sq=1, D=128,
+             scale=0.1275, causal=1, dtype=0)
+    a.update(kw)
+    return lib.gqa_paged_split_first_launch(
+        a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"], a["tstride"], a["lens"], a["bs"],
+        a["max_len"], a["ws"], a["splits"], a["B"], a["Hq"], a["Hkv"], a["Sq"], a["D"], a["scale"],
+        a["causal"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(bs=48), -8), (dict(bs=0), -8), (dict(bs=1 << 17), -8),   # block size
+    (dict(tstride=15), -8),                                        # 15 * 64 < 1024 keys
+    (dict(splits=0), -5), (dict(splits=2048), -5),
+    (dict(lens=None), -7), (dict(table=None), -7), (dict(ws=None), -7),
+    (dict(lens=ctypes.c_void_p((1 << 20) + 2)), -4),
+    (dict(table=ctypes.c_void_p((1 << 20) + 2)), -4),
+    (dict(ws=ctypes.c_void_p((1 << 20) + 4)), -4),
+    (dict(ks=(ctypes.c_int64 * 4)(64 * 8 * 128, 8 * 128, 128, 2)), -4),
+    (dict(D=96), -2), (dict(dtype=5), -3), (dict(Hq=30), -1), (dict(max_len=-1), -1),
+])
+def test_paged_first_validation(lib, kw, code):
+    assert _paged(lib, **kw) == code
+
+
+def test_paged_first_empty_is_noop(lib):
+    assert _paged(lib, B=0, q=None, k=None, v=None, table=None, lens=None, ws=None) == 0
+    assert _paged(lib, Sq=0, q=None, k=None, v=None, table=None, lens=None, ws=None) == 0
+
+
+def _write(lib, **kw):
+    i3 = ctypes.c_int64 * 3
+    a = dict(k=_FAKE, ks=i3(8 * 128, 128, 1), v=_FAKE, vs=i3(8 * 128, 128, 1), kc=_FAKE, kcs=_C4, vc=_FAKE,
+             vcs=_C4, slots=_FAKE, n=4, Hkv=8, D=128, bs=64, dtype=0)
+    a.update(kw)
+    return lib.gqa_paged_cache_write_launch(a["k"], a["ks"], a["v"], a["vs"], a["kc"], a["kcs"], a["vc"],
+                                            a["vcs"], a["slots"], a["n"], a["Hkv"], a["D"], a["bs"],
+                                            a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(bs=6), -8), (dict(bs=0), -8),
+    (dict(D=80), -2), (dict(dtype=2), -3), (dict(n=-1), -1), (dict(Hkv=0), -1),
+    (dict(slots=None), -7), (dict(k=None), -7), (dict(kc=None), -7),
+    (dict(slots=ctypes.c_void_p((1 << 20) + 4)), -4),
+    (dict(ks=(ctypes.c_int64 * 3)(8 * 128, 128, 2)), -4),
+    (dict(vs=(ctypes.c_int64 * 3)(8 * 128, 100, 1)), -4),
+    (dict(v=ctypes.c_void_p((1 << 20) + 8)), -4),
+])
+def test_cache_write_validation(lib, kw, code):
+    assert _write(lib, **kw) == code
+
+
+def test_cache_write_empty_is_noop(lib):
+    assert _write(lib, n=0, k=None, v=None, slots=None) == 0
+
+
+def test_strerror_block(lib):
+    assert b"block_size" in lib.gqa_strerror(-8)
+
+
+# ---------------------------------------------------------------------------
+# Split sizing
+# ---------------------------------------------------------------------------
+def test_paged_splits():
+    from gqa_kernels.paged import paged_splits
+    # one 32-row block per kv head: 8 workgroups per split, 512 targeted
+    assert paged_splits(1, 32, 8, 1, 131072, 256) == 64
+    assert paged_splits(64, 32, 8, 1, 4096, 256) == 1
+    assert paged_splits(1, 32, 8, 1, 300, 256) == 1
+    for L in (256, 1000, 5000, 1 << 20):
+        for B in (1, 3, 16):
+            s = paged_splits(B, 32, 8, 1, L, 256)
+            assert s & (s - 1) == 0
+            assert s == 1 or -(-L // s) >= 256
+
+
+# ---------------------------------------------------------------------------
+# Block allocator (CPU tensors: no kernel involved)
+# ---------------------------------------------------------------------------
+def _cache(num_blocks=8, bs=4):
+    from gqa_kernels.paged import PagedKVCache
+    return PagedKVCache(num_blocks, bs, 2, 64, dtype=torch.float32, device="cpu")
+
+
+def test_reserve_allocates_blocks_and_slots():
+    c = _cache()
+    c.add_sequence("a")
+    s1 = c.reserve("a", 6)
+    assert c.seq_len("a") == 6 and len(c.blocks("a")) == 2
+    b0, b1 = c.blocks("a")
+    assert s1 == [b0 * 4 + j for j in range(4)] + [b1 * 4, b1 * 4 + 1]
+    s2 = c.reserve("a", 3)
+    b2 = c.blocks("a")[2]
+    assert s2 == [b1 * 4 + 2, b1 * 4 + 3, b2 * 4]
+    assert c.num_free_blocks() == 5
+    assert c.reserve("a", 0) == [] and c.seq_len("a") == 9
+
+
+def test_fork_shares_blocks_and_copies_partial_block_on_write():
+    c = _cache()
+    c.add_sequence("p")
+    slots = c.reserve("p", 6)  # one full block + 2 slots of a second
+    for i, s in enumerate(slots):
+        c.kv[:, s // 4, s % 4] = float(i + 1)
+    c.fork("p", "x")
+    c.fork("p", "y")
+    assert c.blocks("x") == c.blocks("p") and c.num_free_blocks() == 6
+    sx = c.reserve("x", 1)
+    # x's partly filled last block was copied; its full block is still shared
+    assert c.blocks("x")[0] == c.blocks("p")[0] and c.blocks("x")[1] != c.blocks("p")[1]
+    nb = c.blocks("x")[1]
+    assert sx == [nb * 4 + 2]
+    assert torch.equal(c.kv[:, nb, :2], c.kv[:, c.blocks("p")[1], :2])
+    c.kv[:, nb, 2] = 99.0
+    assert (c.kv[:, c.blocks("p")[1], 2] == 0).all()  # the prefix block is untouched
+    # y still shares p's partial block until it writes
+    assert c.blocks("y") == c.blocks("p")
+
+
+def test_free_returns_blocks_at_last_reference():
+    c = _cache()
+    c.add_sequence("p")
+    c.reserve("p", 8)  # two full blocks
+    c.fork("p", "x")
+    c.reserve("x", 1)  # full blocks are shared as they are: one new block
+    assert c.num_free_blocks() == 5
+    c.free("p")
+    assert c.num_free_blocks() == 5  # x still holds the prefix blocks
+    c.free("x")
+    assert c.num_free_blocks() == 8
+
+
+def test_out_of_blocks_raises_without_changes():
+    c = _cache(num_blocks=3)
+    c.add_sequence("a")
+    c.reserve("a", 10)
+    c.fork("a", "b")
+    with pytest.raises(RuntimeError, match="out of blocks"):
+        c.reserve("b", 3)  # copy of the shared partial block + 1 more block > 0 free
+    assert c.seq_len("b") == 10 and c.blocks("b") == c.blocks("a") and c.num_free_blocks() == 0
+
+
+def test_block_table_and_seq_lens():
+    c = _cache()
+    for s, n in (("a", 5), ("b", 1), ("c", 0)):
+        c.add_sequence(s)
+        c.reserve(s, n)
+    t = c.block_table(["a", "b", "c"])
+    assert t.dtype == torch.int32 and tuple(t.shape) == (3, 2)
+    assert t[0].tolist() == c.blocks("a") and t[1, 0] == c.blocks("b")[0] and t[2].tolist() == [0, 0]
+    assert c.seq_lens(["a", "b", "c"]).tolist() == [5, 1, 0]
+
+
+def test_layer_arguments():
+    from gqa_kernels.paged import GQAPagedAttention
+    layer = GQAPagedAttention(32, 128, num_kv_heads=8)
+    assert layer.scale == 128 ** -0.5 and layer.num_kv_heads == 8
+    with pytest.raises(AssertionError):
+        GQAPagedAttention(32, 96, num_kv_heads=8)
+    with pytest.raises(AssertionError):
+        GQAPagedAttention(30, 128, num_kv_heads=8)
