@@ -45,6 +45,11 @@ bool rows_fit_32bit(int seq_kv, const int64_t st[4]) {
 
 TensorRef ref(const void* ptr, const int64_t st[4]) { return TensorRef{ptr, st[0], st[1], st[2]}; }
 
+// A paged cache (num_blocks, block_size, heads, D) as the kernels address it:
+// sb = block stride, sh = head stride, ss = slot stride (the slot plays the
+// role of the sequence position).
+TensorRef cache_ref(const void* ptr, const int64_t st[4]) { return TensorRef{ptr, st[0], st[2], st[1]}; }
+
 int to_code(hipError_t e) { return e == hipSuccess ? GQA_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -169,6 +174,7 @@ int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void*
   p.splits = splits;
   p.chunk = (seq_kv + splits - 1) / splits;
   p.n_rblk = (G * seq_q + 31) / 32;
+  p.rotate = p.k.ss == head_dim && p.v.ss == head_dim;
   p.counters = nullptr;
   p.o = TensorRef{nullptr, 0, 0, 0};
   p.lse = nullptr;
@@ -201,8 +207,8 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const
   const int G = num_heads / num_kv_heads;
   gqa::SplitParams p{};
   p.q = ref(q, q_stride);
-  p.k = ref(k_cache, k_cache_stride);
-  p.v = ref(v_cache, v_cache_stride);
+  p.k = cache_ref(k_cache, k_cache_stride);
+  p.v = cache_ref(v_cache, v_cache_stride);
   p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, G, scale_log2, causal ? 1 : 0};
   const size_t rows = (size_t)batch * num_heads * seq_q * splits;
   p.ws_acc = workspace;
@@ -222,6 +228,7 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const
   int shift = 0;
   while ((1 << shift) < block_size) ++shift;
   p.block_shift = shift;
+  p.rotate = p.k.ss == head_dim && p.v.ss == head_dim;
   return to_code(gqa::launch_paged_split_first(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
@@ -252,8 +259,8 @@ int gqa_paged_cache_write_launch(const void* k, const int64_t k_stride[3], const
   p.k_sh = k_stride[1];
   p.v_st = v_stride[0];
   p.v_sh = v_stride[1];
-  p.kc = ref(k_cache, k_cache_stride);
-  p.vc = ref(v_cache, v_cache_stride);
+  p.kc = cache_ref(k_cache, k_cache_stride);
+  p.vc = cache_ref(v_cache, v_cache_stride);
   p.slots = slot_mapping;
   p.n_tokens = num_tokens;
   p.Hkv = num_kv_heads;
@@ -304,6 +311,7 @@ int fused_impl(const void* q, const int64_t q_stride[4], const void* k, const in
   p.splits = splits;
   p.chunk = (seq_kv + splits - 1) / splits;
   p.n_rblk = (G * seq_q + 31) / 32;
+  p.rotate = p.k.ss == head_dim && p.v.ss == head_dim;
   p.counters = counters;
   p.o = ref(o, o_stride);
   p.lse = lse;

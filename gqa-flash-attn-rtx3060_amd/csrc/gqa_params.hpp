@@ -46,13 +46,16 @@ struct SplitParams {
   float* lse;  // optional, fused combine only: as FwdParams::lse
   // Paged K/V cache (gqa_paged_split_first_launch only): k/v point at a
   // (num_blocks, block_size, Hkv, D) cache with sb = block stride, ss = slot
-  // stride, sh = head stride; key j of sequence b is slot j % block_size of
+  // stride, sh = head stride (note: not the dimension order); key j of sequence b is slot j % block_size of
   // block block_table[b * table_stride + j / block_size]; sequence b has
   // seq_lens[b] keys (dm.Skv is the longest).
   const int* block_table;
   const int* seq_lens;
   int table_stride;
   int block_shift;  // log2(block_size)
+  // Stagger the tile order of the splits (set when each head's K and V rows
+  // are consecutive: key stride == head_dim).
+  int rotate;
 };
 
 // Split-KV combine: one workgroup per (b, q head, query row).

@@ -87,7 +87,9 @@ __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb
     float l = 0.f;
     for (int sp = 0; sp < S; ++sp) l += ma[t * S + sp] * la[t * S + sp];
     lst[t] = l;
-    if (p.lse != nullptr) p.lse[row_index(t) / S] = (mst[t] + __log2f(l)) * kLn2;
+    // LSE of a row with no visible key is -inf (its o stays NaN).
+    if (p.lse != nullptr)
+      p.lse[row_index(t) / S] = mst[t] == -__builtin_inff() ? -__builtin_inff() : (mst[t] + __log2f(l)) * kLn2;
   }
 
   // Split groups: enough work items (<= 1024) to keep many loads in flight.
@@ -205,23 +207,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float l_run = 0.f;
   const float c = dm.c;
 
+  // Tile order.  With one head's keys in consecutive rows, every workgroup
+  // would otherwise stream its chunk from the same relative offset in lock
+  // step with the others (chunks are equally long and equally aligned),
+  // which concentrates the concurrent reads on a subset of the HBM channels;
+  // starting splits s = 0..3 (mod 4) a quarter of the chunk apart spreads
+  // them (~11% faster decode at 131072 keys).  The online softmax does not
+  // depend on the order.
+  const int rot = (p.rotate && ntiles >= 4) ? (s & 3) * (ntiles >> 2) : 0;
+  auto tile_key = [&](int i) {
+    int j = i + rot;
+    if (j >= ntiles) j -= ntiles;
+    return c0 + j * kSplitTileKeys;
+  };
+
   SubTileRegs<D> R0, R1;
   if (ntiles > 0) {
-    load_subtile<D, T, true>(R0, kr, vr, p.k.ss, p.v.ss, c0, c1, t);
-    load_subtile<D, T, true>(R1, kr, vr, p.k.ss, p.v.ss, c0 + 64, c1, t);
+    load_subtile<D, T, true>(R0, kr, vr, p.k.ss, p.v.ss, tile_key(0), c1, t);
+    load_subtile<D, T, true>(R1, kr, vr, p.k.ss, p.v.ss, tile_key(0) + 64, c1, t);
   }
   const int sub = wave >> 1, mb = wave & 1;
   const char* mytile = smem + sub * ST::kBytes;
 
   for (int it = 0; it < ntiles; ++it) {
-    const int key0 = c0 + it * kSplitTileKeys;
+    const int key0 = tile_key(it);
     __syncthreads();  // previous tile fully consumed
     store_subtile<D>(smem, R0, t);
     store_subtile<D>(smem + ST::kBytes, R1, t);
     __syncthreads();
     if (it + 1 < ntiles) {
-      load_subtile<D, T, true>(R0, kr, vr, p.k.ss, p.v.ss, key0 + kSplitTileKeys, c1, t);
-      load_subtile<D, T, true>(R1, kr, vr, p.k.ss, p.v.ss, key0 + kSplitTileKeys + 64, c1, t);
+      load_subtile<D, T, true>(R0, kr, vr, p.k.ss, p.v.ss, tile_key(it + 1), c1, t);
+      load_subtile<D, T, true>(R1, kr, vr, p.k.ss, p.v.ss, tile_key(it + 1) + 64, c1, t);
     }
 
     const int kb0 = key0 + 32 * wave;  // this wave's 32 keys
@@ -389,8 +405,10 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
     const int pos = row % p.Sq;
     const int bh = row / p.Sq;
     const int h = bh % p.Hq, b = bh / p.Hq;
-    // Optional LSE side output (natural log; m* and l* are log2-domain).
-    if (p.lse != nullptr && d4 == 0) p.lse[row] = (mstar + __log2f(l)) * kLn2;
+    // Optional LSE side output (natural log; m* and l* are log2-domain);
+    // -inf for a row with no visible key (whose o stays NaN).
+    if (p.lse != nullptr && d4 == 0)
+      p.lse[row] = mstar == -__builtin_inff() ? -__builtin_inff() : (mstar + __log2f(l)) * kLn2;
     T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh +
               (int64_t)pos * p.o.ss;
     u32x2 x;

@@ -23,10 +23,12 @@ def _need_gpu():
         pytest.skip("needs a GPU")
 
 
-def _paged_inputs(B, Hq, Hkv, Sq, lens, D, block_size, dtype, seed, spare_blocks=5, width_pad=2):
+def _paged_inputs(B, Hq, Hkv, Sq, lens, D, block_size, dtype, seed, spare_blocks=5, width_pad=2, hnd=False):
     """Random q and a paged cache holding `lens[b]` keys per sequence at a
     shuffled block assignment (unused blocks and table entries hold junk that
-    must never be read: NaN in the cache, 0 in the table)."""
+    must never be read: NaN in the cache, 0 in the table).  hnd: the caches
+    are (num_blocks, block_size, Hkv, D) views of (num_blocks, Hkv,
+    block_size, D) storage."""
     g = torch.Generator().manual_seed(seed)
     per = [-(-n // block_size) for n in lens]
     nblk = sum(per) + spare_blocks
@@ -45,6 +47,9 @@ def _paged_inputs(B, Hq, Hkv, Sq, lens, D, block_size, dtype, seed, spare_blocks
             vc[table[b, j // block_size].long(), j % block_size] = v
     q = torch.randn(B, Hq, Sq, D, generator=g)
     q, kc, vc = (t.to(dtype) for t in (q, kc, vc))
+    if hnd:
+        kc = kc.transpose(1, 2).contiguous().transpose(1, 2)
+        vc = vc.transpose(1, 2).contiguous().transpose(1, 2)
     seq_lens = torch.tensor(lens, dtype=torch.int32)
     return q, kc, vc, table, seq_lens
 
@@ -81,6 +86,21 @@ def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, caus
     torch.cuda.synchronize()
     _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype)
     _check(o2, None, q, kc, vc, table, seq_lens, causal, dtype)
+
+
+@pytest.mark.parametrize("bs,causal", [(16, True), (128, True), (64, False)])
+def test_paged_attention_head_major_cache(bs, causal):
+    """Caches stored (num_blocks, Hkv, block_size, D): each head's rows of a
+    block are consecutive (the layout the split kernel streams fastest)."""
+    from gqa_kernels.paged import paged_attention
+    q, kc, vc, table, seq_lens = _paged_inputs(3, 32, 8, 2, [4000, 130, 1111], 128, bs, torch.bfloat16,
+                                               seed=bs, hnd=True)
+    assert kc.stride(1) == 128
+    kd, vd = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (kc, vc))
+    o, lse = paged_attention(q.to(DEV), kd, vd, table.to(DEV), seq_lens.to(DEV), causal, max_seq_len=4000,
+                             return_lse=True)
+    torch.cuda.synchronize()
+    _check(o, lse, q, kc, vc, table, seq_lens, causal, torch.bfloat16)
 
 
 @pytest.mark.parametrize("splits", [1, 3, 16])
@@ -182,12 +202,13 @@ def test_prefix_cache_shared_across_sequences():
     assert cache.num_blocks - cache.num_free_blocks() == used + 6
 
 
-def test_vllm_shaped_layer_decode_and_chunk():
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+def test_vllm_shaped_layer_decode_and_chunk(layout):
     from gqa_kernels.paged import GQAPagedAttention, PagedAttentionMetadata, PagedKVCache
     Hq, Hkv, D, bs = 32, 8, 128, 16
     dt = torch.bfloat16
     g = torch.Generator().manual_seed(13)
-    cache = PagedKVCache(400, bs, Hkv, D, dtype=dt, device=DEV)
+    cache = PagedKVCache(400, bs, Hkv, D, dtype=dt, device=DEV, layout=layout)
     layer = GQAPagedAttention(Hq, D, scale=0.05, num_kv_heads=Hkv)
     hist = {}
     lens0 = [700, 33, 1500]

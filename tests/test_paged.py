@@ -244,6 +244,21 @@ def test_block_table_and_seq_lens():
     assert c.seq_lens(["a", "b", "c"]).tolist() == [5, 1, 0]
 
 
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+def test_cache_layouts_index_alike(layout):
+    from gqa_kernels.paged import PagedKVCache
+    c = PagedKVCache(4, 8, 2, 64, dtype=torch.float32, device="cpu", layout=layout)
+    assert tuple(c.kv.shape) == (2, 4, 8, 2, 64) and tuple(c.k_cache.shape) == (4, 8, 2, 64)
+    # head-major storage: one head's slots of a block are consecutive rows
+    assert c.k_cache.stride(1) == (64 if layout == "HND" else 128)
+    c.add_sequence(0)
+    c.reserve(0, 10)
+    c.kv[0, c.blocks(0)[1], 1, 1] = 5.0  # key 9, head 1
+    c.fork(0, 1)
+    c.reserve(1, 1)  # copy of the shared partial block
+    assert (c.k_cache[c.blocks(1)[1], 1, 1] == 5.0).all()
+
+
 def test_layer_arguments():
     from gqa_kernels.paged import GQAPagedAttention
     layer = GQAPagedAttention(32, 128, num_kv_heads=8)
