@@ -4,7 +4,8 @@
 Prints ONE JSON line (rank 0).  The headline ``value`` is causal-prefill
 TFLOP/s at the Llama-3.1-8B GQA shape, seq 16384 (B=1, Hq=32, Hkv=8, D=128,
 bf16); the ``decode`` object carries split-KV decode at seq_kv 131072
-(microseconds and HBM GB/s).  Timing follows reference benchmark/run.py:140-154
+(microseconds and HBM GB/s), and ``paged_decode`` the same decode over a
+paged KV cache (gqa_kernels.paged) at two block sizes / in-block layouts.  Timing follows reference benchmark/run.py:140-154
 (untimed warm-up calls, then back-to-back calls of the full public function
 between two events on the launch stream, mean per call).
 
@@ -228,7 +229,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
     ap.add_argument("--sweep", action="store_true", help="also time every BASELINE config")
-    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy"], default=None,
                     help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
                          "device copy, the calibration kernel of the HBM traffic counters")
     args = ap.parse_args()
@@ -313,6 +314,11 @@ def main() -> int:
         del q, kvs
         torch.cuda.empty_cache()
 
+    # ---------------- decode over a paged KV cache ----------------
+    if args.only in (None, "paged"):
+        result["paged_decode"] = paged_decode(torch, max(args.steps * 5, 50), args.warmup * 2, traffic)
+        torch.cuda.empty_cache()
+
     if args.sweep:
         result["sweep"] = sweep(torch, gqa_flash_attn)
 
@@ -322,6 +328,37 @@ def main() -> int:
         result["config"]["workload"] = d["workload"]
     print(json.dumps(result))
     return 0
+
+
+def paged_decode(torch, steps, warmup, traffic=None):
+    """Decode at seq_kv 131072 over a paged cache (gqa_kernels.paged): one
+    line per (block size, in-block layout), blocks assigned in a random
+    order, two rotating caches as for the contiguous decode."""
+    from gqa_kernels.paged import paged_attention
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn(B, HQ, 1, D, device="cuda", generator=g).to(torch.bfloat16)
+    lens = torch.full((B,), DECODE_S, dtype=torch.int32, device="cuda")
+    by = hbm_bytes(B, HQ, HKV, 1, DECODE_S, D)
+    out = []
+    for bs, layout in ((64, "HND"), (16, "NHD")):
+        nblk = B * DECODE_S // bs
+        caches = []
+        for _ in range(2):
+            shape = (nblk, HKV, bs, D) if layout == "HND" else (nblk, bs, HKV, D)
+            kc, vc = (torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16) for _ in range(2))
+            if layout == "HND":
+                kc, vc = kc.transpose(1, 2), vc.transpose(1, 2)
+            table = torch.randperm(nblk, device="cuda", generator=g).to(torch.int32).view(B, -1)
+            caches.append((kc, vc, table))
+        ms = _time(torch, lambda i: paged_attention(q, *caches[i % 2], lens, True, max_seq_len=DECODE_S),
+                   steps, warmup)
+        out.append({"workload": f"paged causal GQA decode B={B} Hq={HQ} Hkv={HKV} D={D} seq_q=1 "
+                                f"seq_kv={DECODE_S} block_size={bs} layout={layout}",
+                    "us": ms * 1e3, "gbs": by / (ms * 1e-3) / 1e9,
+                    "frac_of_hbm_peak": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                    "traffic": _traffic_bytes(traffic, f"paged_bs{bs}_{layout}")})
+        del caches
+    return out
 
 
 def sweep(torch, gqa_flash_attn):
