@@ -210,6 +210,18 @@ def _traffic_bytes(traffic, workload):
     return traffic["workloads"][workload]["hbm_bytes_per_call"]
 
 
+def gemm_ceiling(torch, n=16384, steps=5, warmup=2):
+    """bf16 GEMM n x n x n through torch.matmul (hipBLASLt): the practical
+    dense-MFMA ceiling of this GPU, for comparison with the published peak."""
+    g = torch.Generator(device="cuda").manual_seed(7)
+    a = torch.randn(n, n, device="cuda", generator=g).to(torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", generator=g).to(torch.bfloat16)
+    ms = _time(torch, lambda i: torch.matmul(a, b), steps, warmup)
+    del a, b
+    return {"kernel": f"torch.matmul bf16 {n}x{n}x{n} (hipBLASLt)", "ms": ms,
+            "tflops": 2 * n ** 3 / (ms * 1e-3) / 1e12}
+
+
 def copy_calibration(torch, steps, warmup):
     """A plain device copy of 1 GiB (torch's copy kernel): reads and writes
     exactly 2^30 bytes per launch, the reference point for the HBM traffic
@@ -229,9 +241,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
     ap.add_argument("--sweep", action="store_true", help="also time every BASELINE config")
-    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm"], default=None,
                     help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
-                         "device copy, the calibration kernel of the HBM traffic counters")
+                         "device copy, the calibration kernel of the HBM traffic counters; 'gemm' "
+                         "a 16384^3 bf16 library GEMM, the practical MFMA ceiling of the box")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -260,6 +273,9 @@ def main() -> int:
     if args.only == "copy":
         print(json.dumps(copy_calibration(torch, args.steps, args.warmup)))
         return 0
+    if args.only == "gemm":
+        print(json.dumps(gemm_ceiling(torch)))
+        return 0
 
     traffic = _load_traffic()
 
@@ -287,6 +303,13 @@ def main() -> int:
         if not args.skip_cpu:
             result["cpu_baseline"] = cpu_baseline(torch, q, k, v)
         del q, k, v, kvs
+        torch.cuda.empty_cache()
+        # Context for `peak`: what the vendor GEMM reaches on this box (the
+        # shader clock runs well below the 2.4 GHz the published peak assumes
+        # under sustained MFMA load).
+        gemm = gemm_ceiling(torch)
+        result["roofline"]["gemm_ceiling"] = gemm
+        result["roofline"]["frac_of_gemm_ceiling"] = tflops / gemm["tflops"]
         torch.cuda.empty_cache()
 
     # ---------------- decode ----------------
