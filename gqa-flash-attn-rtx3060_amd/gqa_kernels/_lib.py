@@ -109,9 +109,20 @@ def check(code: int) -> None:
         raise GQAError(f"libgqa_hip error {code}: {msg}")
 
 
+# C stride arrays by stride tuple: the launchers copy the strides before they
+# return, so one array can serve every call with the same layout.
+_stride_arrays: dict = {}
+
+
 def strides(t) -> "ctypes.Array":
     """The 4 element strides of a torch tensor as a C int64[4]."""
-    return _i64x4(*t.stride())
+    st = t.stride()
+    arr = _stride_arrays.get(st)
+    if arr is None:
+        if len(_stride_arrays) > 4096:
+            _stride_arrays.clear()
+        arr = _stride_arrays[st] = _i64x4(*st)
+    return arr
 
 
 def strides3(t) -> "ctypes.Array":
