@@ -16,7 +16,7 @@ namespace {
 using gqa::Dims;
 using gqa::TensorRef;
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -99,25 +99,36 @@ namespace {
 int fwd_impl(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4], const void* v,
              const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse, int batch, int num_heads,
              int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2, int causal, int dtype,
-             void* stream) {
+             void* stream, int n_split = 0, float* part_ws = nullptr, int* part_cnt = nullptr) {
   int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
   if (rc) return rc;
   const int G = num_heads / num_kv_heads;
   if (G > gqa::kFwdRows) return GQA_E_GROUP;
+  const int block_m = gqa::kFwdRows / G;
+  const int n_mblk = (seq_q + block_m - 1) / block_m;
+  if (n_split < 0 || n_split > n_mblk) return GQA_E_SPLITS;
   if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (n_split > 0) {
+    if (part_ws == nullptr || part_cnt == nullptr) return GQA_E_NULL;
+    if ((reinterpret_cast<uintptr_t>(part_ws) & 15u) != 0 || (reinterpret_cast<uintptr_t>(part_cnt) & 3u) != 0)
+      return GQA_E_STRIDE;
+  }
   if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
   if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
   if (seq_kv > 0 && (!rows_fit_32bit(seq_kv, k_stride) || !rows_fit_32bit(seq_kv, v_stride))) return GQA_E_STRIDE;
 
-  gqa::FwdParams p;
+  gqa::FwdParams p{};
   p.q = ref(q, q_stride);
   p.k = ref(k, k_stride);
   p.v = ref(v, v_stride);
   p.o = ref(o, o_stride);
   p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, G, scale_log2, causal ? 1 : 0};
-  p.block_m = gqa::kFwdRows / G;
-  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  p.block_m = block_m;
+  p.n_mblk = n_mblk;
   p.lse = lse;
+  p.n_split = n_split;
+  p.part_ws = part_ws;
+  p.part_cnt = part_cnt;
   return to_code(gqa::launch_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
@@ -146,6 +157,26 @@ int gqa_fwd_lse_launch(const void* q, const int64_t q_stride[4], const void* k, 
   if (rc && batch > 0 && seq_q > 0) return rc;
   return fwd_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, batch, num_heads, num_kv_heads,
                   seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
+}
+
+size_t gqa_fwd_split_workspace_bytes(int batch, int num_kv_heads, int head_dim, int n_split) {
+  if (batch <= 0 || num_kv_heads <= 0 || n_split <= 0 || (head_dim != 64 && head_dim != 128)) return 0;
+  return (size_t)batch * num_kv_heads * n_split * 2 * gqa::kFwdPartFloats(head_dim) * sizeof(float);
+}
+
+size_t gqa_fwd_split_counters_count(int batch, int num_kv_heads, int n_split) {
+  if (batch <= 0 || num_kv_heads <= 0 || n_split <= 0) return 0;
+  return (size_t)batch * num_kv_heads * n_split;
+}
+
+int gqa_fwd_split_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                         const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse,
+                         float* workspace, int* counters, int n_split, int batch, int num_heads, int num_kv_heads,
+                         int seq_q, int seq_kv, int head_dim, float scale_log2, int causal, int dtype,
+                         void* stream) {
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  return fwd_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, batch, num_heads, num_kv_heads, seq_q,
+                  seq_kv, head_dim, scale_log2, causal, dtype, stream, n_split, workspace, counters);
 }
 
 int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],

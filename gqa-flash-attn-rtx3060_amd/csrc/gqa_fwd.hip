@@ -245,12 +245,24 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   const int i = lane & 31, hh = lane >> 5;
 
   // Work item: heavy (late) query blocks first under causal, and every XCD
-  // gets a contiguous range of items (same kv head -> same L2).
-  const int total = p.n_mblk * dm.Hkv * dm.B;
+  // gets a contiguous range of items (same kv head -> same L2).  With a key
+  // split, the n_split heaviest blocks of each (b, kv head) come as two
+  // items: first the upper halves of their key ranges, then (in the usual
+  // order) the lower halves and the unsplit blocks.
+  const int n_items = p.n_mblk + p.n_split;
+  const int total = n_items * dm.Hkv * dm.B;
   const int w = xcd_remap(blockIdx.x, total);
-  const int bh = w / p.n_mblk;
-  const int mrank = w - bh * p.n_mblk;
-  const int pid_m = dm.causal ? (p.n_mblk - 1 - mrank) : mrank;
+  const int bh = w / n_items;
+  const int idx = w - bh * n_items;
+  int pid_m, part;  // part: -1 whole key range, 0 lower half, 1 upper half
+  if (idx < p.n_split) {
+    pid_m = p.n_mblk - 1 - idx;
+    part = 1;
+  } else {
+    const int mrank = idx - p.n_split;
+    pid_m = dm.causal ? (p.n_mblk - 1 - mrank) : mrank;
+    part = (pid_m >= p.n_mblk - p.n_split) ? 0 : -1;
+  }
   const int b = bh / dm.Hkv, kvh = bh - b * dm.Hkv;
 
   // This lane's query row.
@@ -279,7 +291,11 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   int kv_end = dm.Skv;
   if (dm.causal) kv_end = min(dm.Skv, pos_hi + (dm.Skv - dm.Sq) + 1);
   kv_end = max(kv_end, 0);
-  const int ntiles = (kv_end + ST::kKeys - 1) / ST::kKeys;
+  const int ntiles_all = (kv_end + ST::kKeys - 1) / ST::kKeys;
+  // This item's tiles [tb, tb + ntiles).
+  const int tsplit = ntiles_all >> 1;
+  const int tb = (part == 1) ? tsplit : 0;
+  const int ntiles = (part == 0) ? tsplit : ntiles_all - tb;
   const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
 
   // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
@@ -339,13 +355,14 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   using BT = std::true_type;
   using BF = std::false_type;
 
-  // Prologue: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1) of stage 2.
+  // Prologue: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1) of stage 2
+  // (tile indices relative to tb).
   if (grp == 0) {
-    issue_tile_dma<D>(sk0, rk, 0u, kssb, koff, gw);
-    issue_tile_dma<D>(sk1, rk, (uint32_t)ST::kKeys * kssb, kssb, koff, gw);
+    issue_tile_dma<D>(sk0, rk, (uint32_t)(tb * ST::kKeys) * kssb, kssb, koff, gw);
+    issue_tile_dma<D>(sk1, rk, (uint32_t)((tb + 1) * ST::kKeys) * kssb, kssb, koff, gw);
   } else {
-    issue_tile_dma<D>(sv1, rv, 0u, vssb, voff, gw);
-    issue_tile_dma<D>(sv2, rv, (uint32_t)ST::kKeys * vssb, vssb, voff, gw);
+    issue_tile_dma<D>(sv1, rv, (uint32_t)(tb * ST::kKeys) * vssb, vssb, voff, gw);
+    issue_tile_dma<D>(sv2, rv, (uint32_t)((tb + 1) * ST::kKeys) * vssb, vssb, voff, gw);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // these loads and Q
   phase_barrier();
@@ -401,19 +418,20 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     phase_barrier();
   };
 
-  // Softmax phase of tile tt (ring slot tt % 3).  First issues this wave's
-  // share of the loads two tiles ahead (group A: K(tt+2) into stage tt+2;
-  // group B: V(tt+2) into stage tt+3), last waits for the loads it issued one
-  // softmax phase earlier.
+  // Softmax phase of tile tt (ring slot tt % 3; tt counts from tb).  First
+  // issues this wave's share of the loads two tiles ahead (group A: K(tt+2)
+  // into stage tt+2; group B: V(tt+2) into stage tt+3), last waits for the
+  // loads it issued one softmax phase earlier.
   auto vphase = [&](auto s3, int tt) {
     constexpr int S3 = decltype(s3)::value;
+    const int ta = tb + tt;  // absolute tile index
     if (grp == 0) {
       issue_tile_dma<D>(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), rk,
-                        (uint32_t)((tt + 2) * ST::kKeys) * kssb, kssb, koff, gw);
+                        (uint32_t)((ta + 2) * ST::kKeys) * kssb, kssb, koff, gw);
     } else {
-      issue_tile_dma<D>(vstage(s3), rv, (uint32_t)((tt + 2) * ST::kKeys) * vssb, vssb, voff, gw);
+      issue_tile_dma<D>(vstage(s3), rv, (uint32_t)((ta + 2) * ST::kKeys) * vssb, vssb, voff, gw);
     }
-    const int key0 = tt * ST::kKeys;
+    const int key0 = ta * ST::kKeys;
     const bool need_mask = (key0 + ST::kKeys > dm.Skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
     if (need_mask) {
 #pragma unroll
@@ -475,6 +493,47 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   // workgroup exits.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
+  // Split query block: publish this half's state (reference max, lane
+  // partial row sum, accumulators, lane-major so each lane of the other
+  // item reads back exactly its own row); the item that completes the
+  // block's counter merges the other half into its registers and writes o.
+  if (part >= 0) {
+    constexpr int PF_ = kFwdPartFloats(D);
+    constexpr int NA = NDB * 16;  // accumulators per lane
+    const int slot = bh * p.n_split + (p.n_mblk - 1 - pid_m);
+    float* mine = p.part_ws + ((int64_t)slot * 2 + part) * PF_;
+    const float* other = p.part_ws + ((int64_t)slot * 2 + (1 - part)) * PF_;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t, acc[db][v]);
+    store_coherent(mine + NA * kFwdThreads + t, m_run);
+    store_coherent(mine + (NA + 1) * kFwdThreads + t, l_run);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+    __syncthreads();
+    __shared__ int s_last;
+    if (t == 0) {
+      const int prev = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (prev == 1);
+      // Both halves have arrived: leave the counter zero for the next call.
+      if (s_last) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const float m_o = load_coherent(other + NA * kFwdThreads + t);
+    const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t);
+    const float mm = fmaxf(m_run, m_o);
+    const float mu = (mm == -__builtin_inff()) ? 0.f : mm;
+    const float a_s = fast_exp2((m_run - mu) * c), a_o = fast_exp2((m_o - mu) * c);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        acc[db][v] = acc[db][v] * a_s + load_coherent(other + (db * 16 + v) * kFwdThreads + t) * a_o;
+    l_run = l_run * a_s + l_o * a_o;
+    m_run = mm;
+  }
+
   // Epilogue: o = acc / l (0/0 = NaN for a row with no visible key, as the
   // reference's acc / l_i at gqa_fwd.py:106).  Optional LSE side output:
   // ln sum_k exp(s_k * D^-0.5) = (m_ref * c + log2 l) * ln 2 (l is relative
@@ -500,7 +559,7 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
 
 template <int DT, int D>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-  const int total = p.n_mblk * p.dm.Hkv * p.dm.B;
+  const int total = (p.n_mblk + p.n_split) * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL((gqa_fwd_kernel<DT, D>), dim3(total), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();

@@ -26,6 +26,14 @@ struct FwdParams {
   int block_m;  // query positions per workgroup (G * block_m <= kFwdRows packed rows)
   int n_mblk;   // ceil(Sq / block_m)
   float* lse;   // optional (nullptr): natural-log LSE per row, contiguous (B, Hq, Sq)
+  // Key-range split of the n_split heaviest query blocks of every (b, kv
+  // head) into two work items (lower and upper half of the block's key
+  // tiles); the second item to finish merges the two partial states.
+  // part_ws: kFwdPartFloats<D> floats per part, two parts per split block;
+  // part_cnt: one zero-initialised counter per split block (left zero).
+  int n_split;
+  float* part_ws;
+  int* part_cnt;
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).
@@ -71,6 +79,9 @@ struct ReduceParams {
 // Packed query rows per single-pass workgroup (8 waves x 32 rows).
 constexpr int kFwdRows = 256;
 constexpr int kFwdThreads = 512;
+// One partial state of a split query block: per lane of the 8 waves, D/2
+// accumulators, the reference max and the lane's partial row sum.
+constexpr int kFwdPartFloats(int D) { return kFwdThreads * (D / 2 + 2); }
 // ln(2): converts a log2-domain log-sum-exp to the natural-log LSE.
 constexpr float kLn2 = 0.693147180559945309f;
 // Keys per single-pass LDS tile, and per split-KV LDS tile.

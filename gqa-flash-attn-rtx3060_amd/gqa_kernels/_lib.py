@@ -18,7 +18,7 @@ DTYPE_FP16 = 1
 
 GQA_MAX_SPLITS = 1024
 GQA_MAX_BLOCK_SIZE = 65536
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -55,6 +55,13 @@ SIGNATURES = {
     "gqa_split_fused_launch": (
         _i,
         [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _p, _i,
+         _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
+    "gqa_fwd_split_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
+    "gqa_fwd_split_counters_count": (ctypes.c_size_t, [_i, _i, _i]),
+    "gqa_fwd_split_launch": (
+        _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _p, _p, _i,
          _i, _i, _i, _i, _i, _i, _f, _i, _i, _p],
     ),
     "gqa_paged_split_first_launch": (

@@ -10,13 +10,14 @@ from __future__ import annotations
 
 import contextlib
 import functools
+import heapq
 import math
 from dataclasses import dataclass
 
 import torch
 
 from . import _lib
-from .gqa_split import split_kv_forward
+from .gqa_split import _counter_buffer, _workspace_buffer, split_kv_forward
 
 __all__ = ["gqa_flash_attn", "Route", "choose_route"]
 
@@ -35,6 +36,18 @@ SPLIT_MIN_TILES = 2
 # Target workgroups per compute unit for the split-KV first pass (the kernel
 # runs two per CU at once; one round of workgroups measured fastest).
 SPLIT_WG_PER_CU = 2
+# Single pass with key-range split of the heaviest causal query blocks: only
+# considered while there are fewer than this many workgroups per CU, and
+# taken when the modelled run time drops by at least FWD_SPLIT_GAIN.
+FWD_SPLIT_MAX_WG_PER_CU = 2
+FWD_SPLIT_GAIN = 0.05
+# Per-work-item overhead of the single-pass kernel (first loads in flight,
+# output, and for split blocks the exchange of the fp32 partial state), in
+# 64-key tile steps, for the run-time model.  Calibrated on MI355X against
+# measured split counts of causal prefill at 1024 and 2048 tokens (best
+# measured: 8 of 16 blocks, -18 %; 8 of 32, -10 %; none at 4096).
+FWD_ITEM_OVERHEAD = 8
+FWD_TILE = 64
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 
@@ -44,14 +57,76 @@ class Route:
     kind: str  # "single" or "split"
     splits: int = 1
     workgroups: int = 0
+    fwd_split: int = 0  # single pass: query blocks per (b, kv head) run as two key halves
 
 
 def _cdiv(a: int, b: int) -> int:
     return -(-a // b)
 
 
+def _fwd_block_tiles(n_mblk: int, block_m: int, seq_q: int, seq_kv: int, causal: bool):
+    """Key tiles of each single-pass query block (gqa_fwd.hip's key range)."""
+    out = []
+    for pid in range(n_mblk):
+        kv_end = seq_kv
+        if causal:
+            pos_hi = min((pid + 1) * block_m, seq_q) - 1
+            kv_end = min(seq_kv, pos_hi + (seq_kv - seq_q) + 1)
+        out.append(_cdiv(max(kv_end, 0), FWD_TILE))
+    return out
+
+
+def fwd_split_makespan(tiles, n_split: int, n_bh: int, cu_count: int, causal: bool = True) -> float:
+    """Modelled run time (tile steps) of the single pass with the n_split
+    heaviest blocks split: work items in the kernel's order (per (b, kv
+    head): upper halves of the split blocks, then every block heavy-first
+    with split blocks as their lower halves), each XCD (cu_count / 8 CUs)
+    taking its contiguous share of items, each CU the next item when free."""
+    n = len(tiles)
+    order = list(range(n - 1, -1, -1)) if causal else list(range(n))
+    items = [tiles[n - 1 - i] - tiles[n - 1 - i] // 2 for i in range(n_split)]
+    for pid in order:
+        items.append(tiles[pid] // 2 if pid >= n - n_split else tiles[pid])
+    per_bh = len(items)
+    total = per_bh * n_bh
+    q, r = divmod(total, 8)
+    per_xcd = max(1, cu_count // 8)
+    worst = 0.0
+    for x in range(8):
+        lo = x * q + min(x, r)
+        heap = [0.0] * per_xcd
+        for w in range(lo, lo + q + (1 if x < r else 0)):
+            heapq.heapreplace(heap, heap[0] + items[w % per_bh] + FWD_ITEM_OVERHEAD)
+        worst = max(worst, max(heap))
+    return worst
+
+
+def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
+                     cu_count: int, causal: bool) -> int:
+    """Query blocks per (b, kv head) to run as two key halves (0: none).
+
+    Only causal blocks differ in length; when there are few workgroups per
+    CU the longest block sets the run time, and splitting the heaviest ones
+    shortens it (fwd_split_makespan picks the count)."""
+    group = num_heads // num_kv_heads
+    block_m = max(1, FWD_ROWS // group)
+    n_mblk = _cdiv(seq_q, block_m)
+    n_bh = batch * num_kv_heads
+    if not causal or n_mblk < 2 or n_mblk * n_bh >= FWD_SPLIT_MAX_WG_PER_CU * cu_count:
+        return 0
+    tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, seq_kv, causal)
+    base = fwd_split_makespan(tiles, 0, n_bh, cu_count)
+    best, best_ns = base, 0
+    for f in (0.25, 0.375, 0.5, 0.625, 0.75, 1.0):
+        ns = max(1, min(n_mblk, round(n_mblk * f)))
+        t = fwd_split_makespan(tiles, ns, n_bh, cu_count)
+        if t < best:
+            best, best_ns = t, ns
+    return best_ns if best <= (1.0 - FWD_SPLIT_GAIN) * base else 0
+
+
 def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
-                 cu_count: int) -> Route:
+                 cu_count: int, causal: bool = True) -> Route:
     """Pick the kernel path for one call (pure function of the shapes).
 
     Counterpart of reference dispatch.py:35-45.  A query block of at most
@@ -73,7 +148,8 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
                and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
             splits *= 2
         return Route("split", splits, base * splits)
-    return Route("single", 1, single_wgs)
+    ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal)
+    return Route("single", 1, single_wgs + ns * num_kv_heads * batch, ns)
 
 
 _route_cached = functools.lru_cache(maxsize=4096)(choose_route)
@@ -131,26 +207,42 @@ def gqa_flash_attn(q, k, v, causal=True, *, return_lse=False):
     q_in = q
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
-    route = _route_cached(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev))
+    route = _route_cached(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev), bool(causal))
 
     # Launch on q's device (a no-op context when it is already current).
     with torch.cuda.device(dev) if dev != torch.cuda.current_device() else contextlib.nullcontext():
         if route.kind == "split":
             return split_kv_forward(q, k, v, causal, route.splits, return_lse=return_lse)
 
-        lib = _lib.load()
         o = torch.empty_like(q_in)  # as dispatch.py:47; contiguous if unusable
         if _kernel_ready(o) is not o:
             o = torch.empty_like(q_in, memory_format=torch.contiguous_format)
-        scale_log2 = (head_dim ** -0.5) * LOG2E
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        common = (batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
-                  scale_log2, int(bool(causal)), _DTYPES[q.dtype], stream)
-        qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),
-                v.data_ptr(), _lib.strides(v), o.data_ptr(), _lib.strides(o))
-        if not return_lse:
-            _lib.check(lib.gqa_fwd_launch(*qkvo, *common))
-            return o
-        lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device)
+        return single_pass_forward(q, k, v, o, causal, route.fwd_split, return_lse)
+
+
+def single_pass_forward(q, k, v, o, causal, fwd_split=0, return_lse=False):
+    """Launch the single-pass kernel on kernel-ready q, k, v and output o;
+    with fwd_split > 0 the heaviest query blocks run as two key halves
+    (gqa_fwd_split_launch; workspace and counters are the stream's cached
+    buffers)."""
+    lib = _lib.load()
+    batch, num_heads, seq_q, head_dim = q.shape
+    _, num_kv_heads, seq_kv, _ = k.shape
+    scale_log2 = (head_dim ** -0.5) * LOG2E
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    common = (batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
+              scale_log2, int(bool(causal)), _DTYPES[q.dtype], stream)
+    qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),
+            v.data_ptr(), _lib.strides(v), o.data_ptr(), _lib.strides(o))
+    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
+    if fwd_split > 0:
+        ws = _workspace_buffer(q.device, stream,
+                               lib.gqa_fwd_split_workspace_bytes(batch, num_kv_heads, head_dim, fwd_split))
+        cnt = _counter_buffer(q.device, stream, lib.gqa_fwd_split_counters_count(batch, num_kv_heads, fwd_split))
+        _lib.check(lib.gqa_fwd_split_launch(*qkvo, None if lse is None else lse.data_ptr(), ws.data_ptr(),
+                                            cnt.data_ptr(), fwd_split, *common))
+    elif lse is None:
+        _lib.check(lib.gqa_fwd_launch(*qkvo, *common))
+    else:
         _lib.check(lib.gqa_fwd_lse_launch(*qkvo, lse.data_ptr(), *common))
-        return o, lse
+    return o if lse is None else (o, lse)

@@ -93,6 +93,32 @@ int gqa_fwd_lse_launch(const void* q, const int64_t q_stride[4],
                        int seq_q, int seq_kv, int head_dim,
                        float scale_log2, int causal, int dtype, void* stream);
 
+/* Single pass with a key-range split of the heaviest query blocks (no
+ * counterpart in the reference; its dispatch.py:35-45 only splits decode).
+ * Under causal masking the query blocks of one (batch, kv head) carry from 1
+ * to seq_kv/64 key tiles, so when there are few blocks per compute unit
+ * (prefill at 2K tokens: 256 blocks for 256 CUs) the longest block sets the
+ * run time.  This entry point runs the n_split heaviest blocks of every
+ * (batch, kv head) as two work items each (lower and upper half of the
+ * block's key tiles); the item that finishes second merges the other's
+ * fp32 partial state (log-sum-exp merge) and writes o (and lse).  Results
+ * equal gqa_fwd_launch's up to float rounding.  n_split in [0, number of
+ * query blocks = ceil(seq_q / (256 / (num_heads / num_kv_heads)))];
+ * workspace: gqa_fwd_split_workspace_bytes() bytes, 16-byte aligned;
+ * counters: gqa_fwd_split_counters_count() int32, zero on the first call and
+ * left zero by every call (one buffer serves all calls on one stream).  lse
+ * may be NULL (no side output) or as in gqa_fwd_lse_launch. */
+size_t gqa_fwd_split_workspace_bytes(int batch, int num_kv_heads, int head_dim, int n_split);
+size_t gqa_fwd_split_counters_count(int batch, int num_kv_heads, int n_split);
+int gqa_fwd_split_launch(const void* q, const int64_t q_stride[4],
+                         const void* k, const int64_t k_stride[4],
+                         const void* v, const int64_t v_stride[4],
+                         void* o, const int64_t o_stride[4], float* lse,
+                         float* workspace, int* counters, int n_split,
+                         int batch, int num_heads, int num_kv_heads,
+                         int seq_q, int seq_kv, int head_dim,
+                         float scale_log2, int causal, int dtype, void* stream);
+
 /* Bytes of fp32 workspace the split-KV path needs for `splits` chunks:
  * acc (batch, num_heads, seq_q, splits, head_dim) followed by m and l
  * (batch, num_heads, seq_q, splits) each — the partial tensors of reference

@@ -1,0 +1,105 @@
+"""GPU parity of the single pass with key-range split of the heaviest causal
+query blocks (gqa_fwd_split_launch): against the CPU oracle on row slices,
+against the unsplit launch (same math, different summation order), with the
+LSE side output, for forced split counts, chunked and fully masked cases,
+and across repeated calls (the counters are left zero)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BASELINE_TOL, REF_TOL, assert_close, errors, make_inputs, oracle, to_np
+from oracle.gqa_oracle import gqa_lse
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+LSE_TOL = 2e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+def _run(q, k, v, causal, n_split, return_lse=False):
+    from gqa_kernels.dispatch import single_pass_forward
+    o = torch.empty_like(q)
+    return single_pass_forward(q, k, v, o, causal, n_split, return_lse)
+
+
+def _rows(sq, n=96):
+    """First, last and evenly spaced query rows (keeps the oracle fast)."""
+    return np.unique(np.concatenate([np.arange(min(sq, 16)), np.linspace(0, sq - 1, n).astype(int),
+                                     np.arange(max(0, sq - 16), sq)]))
+
+
+@pytest.mark.parametrize("S", [512, 1024, 2048])
+def test_auto_split_prefill_matches_oracle(S):
+    from gqa_kernels import gqa_flash_attn
+    from gqa_kernels.dispatch import _cu_count, choose_route
+    route = choose_route(1, 32, 8, S, S, _cu_count(0), True)
+    assert route.kind == "single" and route.fwd_split > 0, route
+    q, k, v = make_inputs(1, 32, 8, S, S, 128, torch.bfloat16, seed=S, device=DEV)
+    print(f"auto split S={S} n_split={route.fwd_split}", flush=True)
+    o, lse = gqa_flash_attn(q, k, v, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    rows = _rows(S)
+    ref = oracle(q, k, v, True, rows=rows)
+    assert_close(to_np(o)[:, :, rows], ref, BASELINE_TOL[torch.bfloat16], f"split S={S}")
+    ref_l = gqa_lse(to_np(q), to_np(k), to_np(v), True, rows=rows)
+    assert np.abs(to_np(lse)[:, :, rows] - ref_l).max() <= LSE_TOL
+    # same result as the unsplit kernel up to summation order
+    o0 = _run(q, k, v, True, 0)
+    torch.cuda.synchronize()
+    assert errors(o, o0)[0] <= 1.6e-2
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D,dtype,n_split", [
+    (1, 32, 8, 1024, 1024, 128, torch.bfloat16, 1),     # only the heaviest block
+    (1, 32, 8, 1024, 1024, 128, torch.bfloat16, 16),    # every block (incl. 1-tile blocks)
+    (2, 16, 2, 700, 700, 64, torch.float16, 5),         # G = 8 (32-position blocks), D = 64, ragged
+    (1, 32, 8, 1024, 1500, 128, torch.bfloat16, 8),     # chunked: seq_q < seq_kv
+    (1, 12, 4, 300, 300, 128, torch.bfloat16, 4),       # G = 3 (85-position blocks)
+])
+def test_forced_split_matches_oracle(B, Hq, Hkv, Sq, Skv, D, dtype, n_split):
+    q, k, v = make_inputs(B, Hq, Hkv, Sq, Skv, D, dtype, seed=n_split + Sq, device=DEV)
+    print(f"forced split {B},{Hq},{Hkv},{Sq},{Skv},{D},{dtype} n_split={n_split}", flush=True)
+    o, lse = _run(q, k, v, True, n_split, return_lse=True)
+    torch.cuda.synchronize()
+    rows = _rows(Sq)
+    ref = oracle(q, k, v, True, rows=rows)
+    assert_close(to_np(o)[:, :, rows], ref, BASELINE_TOL[dtype], "forced split")
+    ref_l = gqa_lse(to_np(q), to_np(k), to_np(v), True, rows=rows)
+    assert np.abs(to_np(lse)[:, :, rows] - ref_l).max() <= LSE_TOL
+
+
+def test_split_at_reference_tolerance_x01_inputs():
+    # the reference's x0.1 inputs and its tighter bf16 tolerance
+    q, k, v = make_inputs(1, 32, 8, 2048, 2048, 128, torch.bfloat16, scale=0.1, seed=3, device=DEV)
+    o = _run(q, k, v, True, 32)
+    torch.cuda.synchronize()
+    rows = _rows(2048)
+    assert_close(to_np(o)[:, :, rows], oracle(q, k, v, True, rows=rows), REF_TOL[torch.bfloat16], "x0.1")
+
+
+def test_split_fully_masked_rows_stay_nan():
+    # causal with seq_q > seq_kv: the first 40 rows see no key
+    q, k, v = make_inputs(1, 8, 8, 296, 256, 128, torch.bfloat16, seed=4, device=DEV)
+    o, lse = _run(q, k, v, True, 2, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isnan(o[:, :, :40]).all() and not torch.isnan(o[:, :, 40:]).any()
+    assert torch.isneginf(lse[:, :, :40]).all() and torch.isfinite(lse[:, :, 40:]).all()
+
+
+def test_split_repeated_calls_leave_counters_zero():
+    from gqa_kernels import gqa_split
+    q, k, v = make_inputs(1, 32, 8, 1024, 1024, 128, torch.bfloat16, seed=6, device=DEV)
+    outs = [_run(q, k, v, True, ns) for ns in (16, 16, 3, 16)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[3])
+    assert errors(outs[0], outs[2])[0] <= 1.6e-2
+    for buf in gqa_split._counters.values():
+        assert int(buf.abs().sum().item()) == 0

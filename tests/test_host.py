@@ -174,6 +174,45 @@ def test_route_baseline_configs():
     assert choose_route(1, 32, 8, 1, 512, cu).kind == "single"
 
 
+def test_fwd_split_choice():
+    from gqa_kernels.dispatch import _fwd_block_tiles, choose_fwd_split, choose_route, fwd_split_makespan
+    cu = 256
+    # few causal blocks per CU: the heaviest blocks are split
+    for S in (512, 1024, 2048):
+        r = choose_route(1, 32, 8, S, S, cu, True)
+        n_mblk = S // 64
+        assert r.kind == "single" and 0 < r.fwd_split <= n_mblk
+        assert r.workgroups == (n_mblk + r.fwd_split) * 8
+        tiles = _fwd_block_tiles(n_mblk, 64, S, S, True)
+        assert fwd_split_makespan(tiles, r.fwd_split, 8, cu) <= 0.95 * fwd_split_makespan(tiles, 0, 8, cu)
+    # enough blocks per CU, non-causal, chunked (uniform blocks): no split
+    assert choose_route(1, 32, 8, 16384, 16384, cu, True).fwd_split == 0
+    assert choose_route(1, 32, 8, 2048, 2048, cu, False).fwd_split == 0
+    assert choose_fwd_split(4, 32, 8, 512, 8192, cu, True) == 0
+    # causal block tiles: block m of a square prefill sees m + 1 tiles
+    assert _fwd_block_tiles(4, 64, 256, 256, True) == [1, 2, 3, 4]
+    assert _fwd_block_tiles(2, 64, 128, 1000, True) == [15, 16]
+    assert _fwd_block_tiles(2, 64, 128, 1000, False) == [16, 16]
+
+
+def test_fwd_split_launch_validation(lib):
+    f = lib.gqa_fwd_split_launch
+    args = lambda lse, ws, cnt, ns: (_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, lse, ws, cnt, ns,
+                                     1, 32, 8, 1024, 1024, 128, 0.1275, 1, 0, None)
+    assert f(*args(None, _FAKE, _FAKE, 17)) == -5   # 1024 / 64 = 16 query blocks
+    assert f(*args(None, _FAKE, _FAKE, -1)) == -5
+    assert f(*args(None, None, _FAKE, 4)) == -7
+    assert f(*args(None, _FAKE, None, 4)) == -7
+    assert f(*args(None, ctypes.c_void_p((1 << 20) + 8), _FAKE, 4)) == -4
+    assert f(*args(None, _FAKE, ctypes.c_void_p((1 << 20) + 2), 4)) == -4
+    assert f(*args(ctypes.c_void_p((1 << 20) + 2), _FAKE, _FAKE, 4)) == -4
+    assert lib.gqa_fwd_split_workspace_bytes(2, 8, 128, 5) == 2 * 8 * 5 * 2 * 512 * (64 + 2) * 4
+    assert lib.gqa_fwd_split_workspace_bytes(1, 8, 64, 3) == 8 * 3 * 2 * 512 * (32 + 2) * 4
+    assert lib.gqa_fwd_split_workspace_bytes(1, 8, 96, 3) == 0
+    assert lib.gqa_fwd_split_counters_count(2, 8, 5) == 80
+    assert lib.gqa_fwd_split_counters_count(2, 8, 0) == 0
+
+
 def test_route_properties():
     from gqa_kernels.dispatch import SPLIT_MIN_TILES, SPLIT_TILE, choose_route
     for skv in (1024, 1500, 4096, 65536, 1 << 20):
