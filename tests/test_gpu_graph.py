@@ -1,0 +1,96 @@
+"""The public path under HIP graph capture (torch.cuda.CUDAGraph): decode
+steps (split-KV, two launches), the fused combine, prefill with and without
+the key split, and paged decode are captured once and replayed several
+times, with eager work and synchronisations between replays; every replay
+must equal the eager result bit for bit (the kernels are deterministic and
+the captured launches see the same inputs)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+def _capture(fn):
+    # Warm-up on a side stream first: the cached workspaces and counters are
+    # created (and zeroed) outside the capture.
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    return g, out
+
+
+def _replays(g, out, expect, n=4):
+    for i in range(n):
+        # eager work between replays (allocations, a reduction, a sync)
+        junk = torch.randn(1 << 16, device=DEV).sum()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        outs = out if isinstance(out, tuple) else (out,)
+        exps = expect if isinstance(expect, tuple) else (expect,)
+        for a, b in zip(outs, exps):
+            assert torch.equal(a, b), f"replay {i} differs from the eager result"
+        del junk
+
+
+@pytest.mark.parametrize("case", ["decode", "decode_lse", "prefill", "prefill_split", "chunked"])
+def test_public_path_in_graph(case):
+    from gqa_kernels import gqa_flash_attn
+    shapes = {"decode": (1, 32, 8, 1, 16384), "decode_lse": (2, 32, 8, 1, 5000),
+              "prefill": (1, 32, 8, 4096, 4096), "prefill_split": (1, 32, 8, 1024, 1024),
+              "chunked": (2, 32, 8, 256, 3000)}
+    B, Hq, Hkv, Sq, Skv = shapes[case]
+    q, k, v = make_inputs(B, Hq, Hkv, Sq, Skv, 128, torch.bfloat16, seed=len(case), device=DEV)
+    lse = case == "decode_lse"
+    print(f"graph {case}", flush=True)
+    fn = lambda: gqa_flash_attn(q, k, v, causal=True, return_lse=lse)
+    expect = fn()
+    torch.cuda.synchronize()
+    expect = tuple(t.clone() for t in expect) if lse else expect.clone()
+    g, out = _capture(fn)
+    _replays(g, out, expect)
+
+
+def test_fused_split_in_graph():
+    from gqa_kernels.gqa_split import split_kv_forward
+    q, k, v = make_inputs(1, 32, 8, 1, 8192, 128, torch.bfloat16, seed=3, device=DEV)
+    fn = lambda: split_kv_forward(q, k, v, True, 32, fused=True)
+    expect = fn().clone()
+    g, out = _capture(fn)
+    _replays(g, out, expect)
+
+
+def test_paged_decode_in_graph():
+    from gqa_kernels.paged import PagedKVCache
+    g0 = torch.Generator().manual_seed(5)
+    cache = PagedKVCache(256, 64, 8, 128, dtype=torch.bfloat16, device=DEV)
+    for s, n in enumerate((3000, 777)):
+        cache.add_sequence(s)
+        cache.append([s], torch.randn(n, 8, 128, generator=g0).to(torch.bfloat16).to(DEV),
+                     torch.randn(n, 8, 128, generator=g0).to(torch.bfloat16).to(DEV))
+    q = torch.randn(2, 32, 1, 128, generator=g0).to(torch.bfloat16).to(DEV)
+    table, lens = cache.block_table([0, 1]), cache.seq_lens([0, 1])
+    from gqa_kernels.paged import paged_attention
+    fn = lambda: paged_attention(q, cache.k_cache, cache.v_cache, table, lens, True, max_seq_len=3000)
+    expect = fn().clone()
+    g, out = _capture(fn)
+    _replays(g, out, expect)
