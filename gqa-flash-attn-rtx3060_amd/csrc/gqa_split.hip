@@ -418,86 +418,6 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   }
 }
 
-// The same combine with every load issued up front: thread (d4, sg) holds the
-// partials of its splits sg, sg + NSG, ... (at most kRegSplitsPerThread) in
-// registers, so the row's single memory round trip overlaps all of them;
-// used when splits <= NSG * kRegSplitsPerThread (64 for D = 128, 128 for
-// D = 64).
-constexpr int kRegSplitsPerThread = 8;
-template <int D>
-constexpr int kReduceRegSplits = (256 / (D / 4)) * kRegSplitsPerThread;
-
-template <int DT, int D>
-__global__ __launch_bounds__(256) void gqa_split_reduce_regs_kernel(ReduceParams p) {
-  using E = Elem<DT>;
-  using T = typename E::T;
-  constexpr int ND4 = D / 4;
-  constexpr int NSG = 256 / ND4;
-  constexpr int K = kRegSplitsPerThread;
-  __shared__ float red_m[4];
-  __shared__ f32x4 red_o[NSG][ND4];
-  __shared__ float red_l[NSG][ND4];
-
-  const int t = threadIdx.x;
-  const int row = blockIdx.x;  // ((b * Hq + h) * Sq + pos)
-  const int S = p.splits;
-  const float* wm = p.ws_m + (int64_t)row * S;
-  const float* wl = p.ws_l + (int64_t)row * S;
-  const float* wa = p.ws_acc + (int64_t)row * S * D;
-  const int d4 = t % ND4, sg = t / ND4;
-
-  float mv[K], lv[K];
-  f32x4 av[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int s = sg + k * NSG;
-    const bool in = s < S;
-    mv[k] = in ? wm[s] : -__builtin_inff();
-    lv[k] = in ? wl[s] : 0.f;
-    av[k] = in ? *reinterpret_cast<const f32x4*>(wa + (int64_t)s * D + 4 * d4) : f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  // m* = max over splits: this thread's, the wave's (its two split groups),
-  // then the 4 waves in LDS.
-  float mx = mv[0];
-#pragma unroll
-  for (int k = 1; k < K; ++k) mx = fmaxf(mx, mv[k]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((t & 63) == 0) red_m[t >> 6] = mx;
-  __syncthreads();
-  const float mstar = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    // exp2(-inf - -inf) = NaN when every chunk is empty, as gqa_split.py:138.
-    const float a = fast_exp2(mv[k] - mstar);
-    l += a * lv[k];
-    o += a * av[k];
-  }
-  red_o[sg][d4] = o;
-  red_l[sg][d4] = l;
-  __syncthreads();
-  if (sg == 0) {
-    for (int k = 1; k < NSG; ++k) {
-      o += red_o[k][d4];
-      l += red_l[k][d4];
-    }
-    const int pos = row % p.Sq;
-    const int bh = row / p.Sq;
-    const int h = bh % p.Hq, b = bh / p.Hq;
-    if (p.lse != nullptr && d4 == 0)
-      p.lse[row] = mstar == -__builtin_inff() ? -__builtin_inff() : (mstar + __log2f(l)) * kLn2;
-    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh +
-              (int64_t)pos * p.o.ss;
-    u32x2 x;
-    x[0] = E::pack2(o[0] / l, o[1] / l);
-    x[1] = E::pack2(o[2] / l, o[3] / l);
-    *reinterpret_cast<u32x2*>(orow + 4 * d4) = x;
-  }
-}
-
 template <int DT, int D, int KV>
 static hipError_t launch_split_first_t(const SplitParams& p, hipStream_t stream) {
   const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * p.n_rblk * p.splits;
@@ -510,10 +430,7 @@ template <int DT, int D>
 static hipError_t launch_split_reduce_t(const ReduceParams& p, hipStream_t stream) {
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
   if (rows <= 0) return hipSuccess;
-  if (p.splits <= kReduceRegSplits<D>)
-    hipLaunchKernelGGL((gqa_split_reduce_regs_kernel<DT, D>), dim3((unsigned)rows), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gqa_split_reduce_kernel<DT, D>), dim3((unsigned)rows), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gqa_split_reduce_kernel<DT, D>), dim3((unsigned)rows), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
