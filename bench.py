@@ -4,8 +4,9 @@
 Prints ONE JSON line (rank 0).  The headline ``value`` is causal-prefill
 TFLOP/s at the Llama-3.1-8B GQA shape, seq 16384 (B=1, Hq=32, Hkv=8, D=128,
 bf16); the ``decode`` object carries split-KV decode at seq_kv 131072
-(microseconds and HBM GB/s), and ``paged_decode`` the same decode over a
-paged KV cache (gqa_kernels.paged) at two block sizes / in-block layouts.  Timing follows reference benchmark/run.py:140-154
+(microseconds and HBM GB/s), ``paged_decode`` the same decode over a paged
+KV cache (gqa_kernels.paged) at two block sizes / in-block layouts, and
+``paged_prefill`` the chunked-prefill shape over a paged cache.  Timing follows reference benchmark/run.py:140-154
 (untimed warm-up calls, then back-to-back calls of the full public function
 between two events on the launch stream, mean per call).
 
@@ -337,9 +338,11 @@ def main() -> int:
         del q, kvs
         torch.cuda.empty_cache()
 
-    # ---------------- decode over a paged KV cache ----------------
+    # ---------------- decode and chunked prefill over a paged KV cache ----------------
     if args.only in (None, "paged"):
         result["paged_decode"] = paged_decode(torch, max(args.steps * 5, 50), args.warmup * 2, traffic)
+        torch.cuda.empty_cache()
+        result["paged_prefill"] = paged_prefill(torch, args.steps, args.warmup)
         torch.cuda.empty_cache()
 
     if args.sweep:
@@ -381,6 +384,33 @@ def paged_decode(torch, steps, warmup, traffic=None):
                     "frac_of_hbm_peak": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                     "traffic": _traffic_bytes(traffic, f"paged_bs{bs}_{layout}")})
         del caches
+    return out
+
+
+def paged_prefill(torch, steps, warmup):
+    """The chunked-prefill BASELINE shape (B=4, 512 new tokens attending 8192
+    keys, causal) over a paged cache (gqa_kernels.paged, single-pass route),
+    128-key HND blocks and 64-key NHD blocks in random order."""
+    from gqa_kernels.paged import paged_attention
+    b, sq, skv = 4, 512, 8192
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn(b, HQ, sq, D, device="cuda", generator=g).to(torch.bfloat16)
+    lens = torch.full((b,), skv, dtype=torch.int32, device="cuda")
+    fl = flops(b, HQ, sq, skv, D)
+    out = []
+    for bs, layout in ((128, "HND"), (64, "NHD")):
+        nblk = b * skv // bs
+        shape = (nblk, HKV, bs, D) if layout == "HND" else (nblk, bs, HKV, D)
+        kc, vc = (torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16) for _ in range(2))
+        if layout == "HND":
+            kc, vc = kc.transpose(1, 2), vc.transpose(1, 2)
+        table = torch.randperm(nblk, device="cuda", generator=g).to(torch.int32).view(b, -1)
+        ms = _time(torch, lambda i: paged_attention(q, kc, vc, table, lens, True, max_seq_len=skv), steps, warmup)
+        out.append({"workload": f"paged causal GQA chunked prefill B={b} Hq={HQ} Hkv={HKV} D={D} seq_q={sq} "
+                                f"seq_kv={skv} block_size={bs} layout={layout}",
+                    "us": ms * 1e3, "tflops": fl / (ms * 1e-3) / 1e12,
+                    "frac_of_mfma_peak": fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS})
+        del kc, vc
     return out
 
 

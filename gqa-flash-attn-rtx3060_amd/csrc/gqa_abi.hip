@@ -16,7 +16,7 @@ namespace {
 using gqa::Dims;
 using gqa::TensorRef;
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -261,6 +261,48 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const
   p.block_shift = shift;
   p.rotate = p.k.ss == head_dim && p.v.ss == head_dim;
   return to_code(gqa::launch_paged_split_first(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4], const void* k_cache,
+                         const int64_t k_cache_stride[4], const void* v_cache, const int64_t v_cache_stride[4],
+                         const int* block_table, int table_stride, const int* seq_lens, int block_size,
+                         int max_seq_len, void* o, const int64_t o_stride[4], float* lse, int batch,
+                         int num_heads, int num_kv_heads, int seq_q, int head_dim, float scale_log2, int causal,
+                         int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
+  if (rc) return rc;
+  const int G = num_heads / num_kv_heads;
+  if (G > gqa::kFwdRows) return GQA_E_GROUP;
+  if (block_size < 64 || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
+    return GQA_E_BLOCK;
+  if (table_stride < 0 || (int64_t)table_stride * block_size < (int64_t)max_seq_len) return GQA_E_BLOCK;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (seq_lens == nullptr) return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0) return GQA_E_STRIDE;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
+  if (max_seq_len > 0) {
+    if (block_table == nullptr) return GQA_E_NULL;
+    if ((reinterpret_cast<uintptr_t>(block_table) & 3u) != 0) return GQA_E_STRIDE;
+    if ((rc = check_tensor(k_cache, k_cache_stride)) || (rc = check_tensor(v_cache, v_cache_stride))) return rc;
+  }
+
+  gqa::FwdParams p{};
+  p.q = ref(q, q_stride);
+  p.k = cache_ref(k_cache, k_cache_stride);
+  p.v = cache_ref(v_cache, v_cache_stride);
+  p.o = ref(o, o_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, G, scale_log2, causal ? 1 : 0};
+  p.block_m = gqa::kFwdRows / G;
+  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  p.lse = lse;
+  p.block_table = block_table;
+  p.seq_lens = seq_lens;
+  p.table_stride = table_stride;
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  p.block_shift = shift;
+  return to_code(gqa::launch_paged_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
 int gqa_paged_cache_write_launch(const void* k, const int64_t k_stride[3], const void* v,

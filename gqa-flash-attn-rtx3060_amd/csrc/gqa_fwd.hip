@@ -218,7 +218,9 @@ __device__ __forceinline__ void mphase_pipe() {
   }
 }
 
-template <int DT, int D>
+// PAGED: K/V tiles come from a paged cache through the block table (one
+// buffer descriptor per 64-key tile, ending at the sequence's last key).
+template <int DT, int D, bool PAGED>
 __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
@@ -264,6 +266,8 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     part = (pid_m >= p.n_mblk - p.n_split) ? 0 : -1;
   }
   const int b = bh / dm.Hkv, kvh = bh - b * dm.Hkv;
+  // Keys of this sequence (paged: its own length, clamped to [0, Skv]).
+  const int skv = PAGED ? min(max(p.seq_lens[b], 0), dm.Skv) : dm.Skv;
 
   // This lane's query row.
   const int r = wave * 32 + i;
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   const int pos = pid_m * p.block_m + ml;
   const bool valid = (g < dm.G) && (pos < dm.Sq);
   const int head = kvh * dm.G + (g < dm.G ? g : 0);
-  const int qpos = pos + (dm.Skv - dm.Sq);
+  const int qpos = pos + (skv - dm.Sq);
 
   u32x4 qreg[NKS];
   {
@@ -288,29 +292,60 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   // Key range of this workgroup.
   const int pos_lo = pid_m * p.block_m;
   const int pos_hi = min(pos_lo + p.block_m, dm.Sq) - 1;
-  int kv_end = dm.Skv;
-  if (dm.causal) kv_end = min(dm.Skv, pos_hi + (dm.Skv - dm.Sq) + 1);
+  int kv_end = skv;
+  if (dm.causal) kv_end = min(skv, pos_hi + (skv - dm.Sq) + 1);
   kv_end = max(kv_end, 0);
   const int ntiles_all = (kv_end + ST::kKeys - 1) / ST::kKeys;
   // This item's tiles [tb, tb + ntiles).
   const int tsplit = ntiles_all >> 1;
   const int tb = (part == 1) ? tsplit : 0;
   const int ntiles = (part == 0) ? tsplit : ntiles_all - tb;
-  const int qpos_lo = pos_lo + (dm.Skv - dm.Sq);
+  const int qpos_lo = pos_lo + (skv - dm.Sq);
 
   // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
   // each ending at the last byte of row seq_kv - 1, and per-lane offsets.
   // The host guarantees (seq_kv + 192) * row stride * 2 < 2^31, so every
   // offset below (up to two tiles past the end) fits 32 bits.
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
-  const char* kbh = static_cast<const char*>(p.k.ptr) + 2 * ((int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh);
-  const char* vbh = static_cast<const char*>(p.v.ptr) + 2 * ((int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbh, (uint32_t)(dm.Skv - 1) * kssb + 2 * D);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, (uint32_t)(dm.Skv - 1) * vssb + 2 * D);
+  const char* kbh = static_cast<const char*>(p.k.ptr) +
+                    2 * ((PAGED ? 0 : (int64_t)b * p.k.sb) + (int64_t)kvh * p.k.sh);
+  const char* vbh = static_cast<const char*>(p.v.ptr) +
+                    2 * ((PAGED ? 0 : (int64_t)b * p.v.sb) + (int64_t)kvh * p.v.sh);
+  // (An empty key range gets an empty descriptor: every load reads zero.)
+  const bool flat = !PAGED && dm.Skv > 0;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbh, flat ? (uint32_t)(dm.Skv - 1) * kssb + 2 * D : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, flat ? (uint32_t)(dm.Skv - 1) * vssb + 2 * D : 0u);
+  const int* table_row = PAGED ? p.block_table + (int64_t)b * p.table_stride : nullptr;
+
   const int lrow = lane / CPR;
   const uint32_t koff =
       (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ ST::gk((gw * ST::RPI + lrow) & 15));
   const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ ST::sv(lrow));
+
+  // Issue this wave's share of K or V tile `tile` (absolute index) into LDS.
+  // Paged: the tile's 64 rows are one run inside one block; its descriptor
+  // starts at the tile's first row and ends at the sequence's last key, so
+  // rows past the sequence (and whole tiles past it, which read no table
+  // entry) load as zeros.
+  auto issue_tile = [&](char* lds, const char* head, __amdgpu_buffer_rsrc_t rsrc, uint32_t rowb, uint32_t off,
+                        int64_t blk_stride, int tile) {
+    if constexpr (PAGED) {
+      const int key0 = tile * ST::kKeys;
+      const int rows = skv - key0;
+      __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
+      if (rows > 0) {
+        const int blk = table_row[key0 >> p.block_shift];
+        const char* base =
+            head + 2 * ((int64_t)blk * blk_stride + (int64_t)(key0 & ((1 << p.block_shift) - 1)) * (rowb >> 1));
+        rt = make_rsrc(base, (uint32_t)(min(rows, ST::kKeys) - 1) * rowb + 2 * D);
+      }
+      issue_tile_dma<D>(lds, rt, 0u, rowb, off, gw);
+    } else {
+      issue_tile_dma<D>(lds, rsrc, (uint32_t)(tile * ST::kKeys) * rowb, rowb, off, gw);
+    }
+  };
+  auto issue_k = [&](char* lds, int tile) { issue_tile(lds, kbh, rk, kssb, koff, p.k.sb, tile); };
+  auto issue_v = [&](char* lds, int tile) { issue_tile(lds, vbh, rv, vssb, voff, p.v.sb, tile); };
 
   // LDS side: per-lane read offsets (the 32-key block, chunk and row offsets
   // of each read are immediates on top of these).  The masks are no-ops on
@@ -358,11 +393,11 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   // Prologue: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1) of stage 2
   // (tile indices relative to tb).
   if (grp == 0) {
-    issue_tile_dma<D>(sk0, rk, (uint32_t)(tb * ST::kKeys) * kssb, kssb, koff, gw);
-    issue_tile_dma<D>(sk1, rk, (uint32_t)((tb + 1) * ST::kKeys) * kssb, kssb, koff, gw);
+    issue_k(sk0, tb);
+    issue_k(sk1, tb + 1);
   } else {
-    issue_tile_dma<D>(sv1, rv, (uint32_t)(tb * ST::kKeys) * vssb, vssb, voff, gw);
-    issue_tile_dma<D>(sv2, rv, (uint32_t)((tb + 1) * ST::kKeys) * vssb, vssb, voff, gw);
+    issue_v(sv1, tb);
+    issue_v(sv2, tb + 1);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // these loads and Q
   phase_barrier();
@@ -426,20 +461,19 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     constexpr int S3 = decltype(s3)::value;
     const int ta = tb + tt;  // absolute tile index
     if (grp == 0) {
-      issue_tile_dma<D>(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), rk,
-                        (uint32_t)((ta + 2) * ST::kKeys) * kssb, kssb, koff, gw);
+      issue_k(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), ta + 2);
     } else {
-      issue_tile_dma<D>(vstage(s3), rv, (uint32_t)((ta + 2) * ST::kKeys) * vssb, vssb, voff, gw);
+      issue_v(vstage(s3), ta + 2);
     }
     const int key0 = ta * ST::kKeys;
-    const bool need_mask = (key0 + ST::kKeys > dm.Skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
+    const bool need_mask = (key0 + ST::kKeys > skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
     if (need_mask) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = key0 + 32 * mb + key_of(v, hh);
-          const bool off = key >= dm.Skv || (dm.causal && key > qpos);
+          const bool off = key >= skv || (dm.causal && key > qpos);
           sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
     }
@@ -557,17 +591,25 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   }
 }
 
-template <int DT, int D>
+template <int DT, int D, bool PAGED>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   const int total = (p.n_mblk + p.n_split) * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D>), dim3(total), dim3(kFwdThreads), 0, stream, p);
+  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PAGED>), dim3(total), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();
 }
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
-  if (dtype == 0) return p.dm.D == 128 ? launch_fwd_t<0, 128>(p, stream) : launch_fwd_t<0, 64>(p, stream);
-  return p.dm.D == 128 ? launch_fwd_t<1, 128>(p, stream) : launch_fwd_t<1, 64>(p, stream);
+  if (dtype == 0)
+    return p.dm.D == 128 ? launch_fwd_t<0, 128, false>(p, stream) : launch_fwd_t<0, 64, false>(p, stream);
+  return p.dm.D == 128 ? launch_fwd_t<1, 128, false>(p, stream) : launch_fwd_t<1, 64, false>(p, stream);
+}
+
+// Requires block_size >= 64 (a 64-key tile lies in one block).
+hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
+  if (dtype == 0)
+    return p.dm.D == 128 ? launch_fwd_t<0, 128, true>(p, stream) : launch_fwd_t<0, 64, true>(p, stream);
+  return p.dm.D == 128 ? launch_fwd_t<1, 128, true>(p, stream) : launch_fwd_t<1, 64, true>(p, stream);
 }
 
 }  // namespace gqa

@@ -34,6 +34,13 @@ struct FwdParams {
   int n_split;
   float* part_ws;
   int* part_cnt;
+  // Paged K/V (gqa_paged_fwd_launch only): k/v as in SplitParams (block,
+  // head and slot strides), block_size >= 64 so a 64-key tile lies in one
+  // block; sequence b has min(seq_lens[b], Skv) keys.
+  const int* block_table;
+  const int* seq_lens;
+  int table_stride;
+  int block_shift;
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).
@@ -104,6 +111,7 @@ struct CacheWriteParams {
 };
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream);
+hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream);  // fused if p.counters
 hipError_t launch_paged_split_first(const SplitParams& p, int dtype, hipStream_t stream);
 hipError_t launch_paged_cache_write(const CacheWriteParams& p, hipStream_t stream);

@@ -6,11 +6,14 @@ K/V for the static prefix and computing attention only over the new tokens";
 "wrapping it in a vLLM-shaped Attention interface is mostly glue code"; "none
 of the above is in this repo").  This module is that step on MI355X:
 
-* ``paged_attention`` — the split-KV kernels of the contiguous decode path
-  reading K/V through a block table (libgqa_hip.so
-  ``gqa_paged_split_first_launch`` + ``gqa_split_reduce[_lse]_launch``), with
-  a length per sequence and the bottom-right causal alignment of
-  ``gqa_flash_attn`` applied per sequence.
+* ``paged_attention`` — the kernels of ``gqa_flash_attn`` reading K/V
+  through a block table, with a length per sequence and the bottom-right
+  causal alignment applied per sequence: for short query blocks (decode,
+  speculative verification) the split-KV pass (libgqa_hip.so
+  ``gqa_paged_split_first_launch`` + ``gqa_split_reduce[_lse]_launch``), for
+  longer ones (chunked prefill against a cached prefix) the single-pass
+  kernel loading each 64-key tile from its block
+  (``gqa_paged_fwd_launch``, blocks of >= 64 keys).
 * ``write_kv`` — store new tokens' K/V at their cache slots
   (``gqa_paged_cache_write_launch``).
 * ``PagedKVCache`` — host-side block allocator with reference-counted blocks:
@@ -55,6 +58,7 @@ _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 _SPLIT_ROWS = 32
 _SPLIT_WG_PER_CU = 2
 _MIN_CHUNK = 256
+_SPLIT_MAX_ROWS = 64  # packed rows per kv head up to which the split-KV pass is used
 
 _cu_lock = threading.Lock()
 _cu_counts: dict = {}
@@ -103,10 +107,19 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> int:
     return block_size
 
 
+def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int) -> str:
+    """"split" (split-KV first pass + combine) for short query blocks, as the
+    contiguous decode route; "single" (the single-pass kernel loading each
+    64-key tile from its block) for longer ones when blocks hold >= 64 keys."""
+    if (num_heads // num_kv_heads) * seq_q <= _SPLIT_MAX_ROWS or block_size < 64:
+        return "split"
+    return "single"
+
+
 def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
                     max_seq_len: Optional[int] = None, scale: Optional[float] = None,
                     splits: Optional[int] = None, return_lse: bool = False,
-                    out: Optional[torch.Tensor] = None):
+                    out: Optional[torch.Tensor] = None, route: Optional[str] = None):
     """GQA attention of q over K/V held in a paged cache.
 
     Args:
@@ -131,6 +144,8 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             (batch, num_heads, seq_q).
         out: optional (batch, num_heads, seq_q, head_dim) tensor of q's dtype
             (any strides with 16-byte aligned rows) to write o into.
+        route: "split" or "single" to force a kernel (default: paged_route;
+            "single" needs block_size >= 64).
 
     Returns:
         o (batch, num_heads, seq_q, head_dim), or (o, lse).
@@ -172,6 +187,17 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
     stream = torch.cuda.current_stream(q.device).cuda_stream
+    route = route or paged_route(num_heads, num_kv_heads, seq_q, block_size)
+    assert route in ("split", "single") and (route == "split" or block_size >= 64)
+    if route == "single":
+        lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
+        _lib.check(lib.gqa_paged_fwd_launch(
+            q.data_ptr(), _lib.strides(q), k_cache.data_ptr(), _lib.strides(k_cache),
+            v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
+            seq_lens.data_ptr(), block_size, max_seq_len, out.data_ptr(), _lib.strides(out),
+            None if lse is None else lse.data_ptr(), batch, num_heads, num_kv_heads, seq_q, head_dim,
+            scale * LOG2E, int(bool(causal)), dtype, stream))
+        return out if lse is None else (out, lse)
     workspace = _workspace_buffer(q.device, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, splits))
     _lib.check(lib.gqa_paged_split_first_launch(
         q.data_ptr(), _lib.strides(q), k_cache.data_ptr(), _lib.strides(k_cache),

@@ -219,6 +219,23 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4],
                                  float scale_log2, int causal, int dtype,
                                  void* stream);
 
+/* Single-pass forward over a paged cache, for query blocks too large for the
+ * split-KV pass (chunked prefill against a cached prefix): the kernel of
+ * gqa_fwd_launch with each 64-key K/V tile loaded from its block, so
+ * block_size must be a power of two >= 64.  Caches, block_table, seq_lens,
+ * max_seq_len and the causal alignment as gqa_paged_split_first_launch;
+ * q and o are (batch, num_heads, seq_q, head_dim); lse may be NULL (no side
+ * output) or as in gqa_fwd_lse_launch. */
+int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4],
+                         const void* k_cache, const int64_t k_cache_stride[4],
+                         const void* v_cache, const int64_t v_cache_stride[4],
+                         const int* block_table, int table_stride,
+                         const int* seq_lens, int block_size, int max_seq_len,
+                         void* o, const int64_t o_stride[4], float* lse,
+                         int batch, int num_heads, int num_kv_heads,
+                         int seq_q, int head_dim,
+                         float scale_log2, int causal, int dtype, void* stream);
+
 /* Store new tokens' K and V into the paged caches:
  * k_cache[slot / block_size, slot % block_size, h, :] = k[t, h, :] (and V)
  * with slot = slot_mapping[t] (int64); tokens whose slot is negative are

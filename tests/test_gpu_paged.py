@@ -88,6 +88,56 @@ def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, caus
     _check(o2, None, q, kc, vc, table, seq_lens, causal, dtype)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,lens,D,bs,dtype,causal,hnd", [
+    (2, 32, 8, 100, [3000, 150], 128, 64, torch.bfloat16, True, False),      # chunk over a prefix
+    (1, 32, 8, 512, [8192], 128, 128, torch.bfloat16, True, True),           # 512-token chunk, HND
+    (3, 64, 8, 40, [1000, 41, 2500], 128, 256, torch.bfloat16, True, False),  # G = 8, sequence == chunk
+    (2, 32, 8, 200, [150, 1000], 128, 64, torch.bfloat16, True, True),       # shorter than the chunk: masked rows
+    (2, 16, 4, 70, [700, 333], 64, 64, torch.float16, False, False),         # D = 64, fp16, non-causal
+])
+def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal, hnd):
+    """Query blocks above the split-KV size take the single-pass kernel with
+    each 64-key tile loaded from its block."""
+    from gqa_kernels.paged import paged_attention, paged_route
+    assert paged_route(Hq, Hkv, Sq, bs) == "single"
+    q, kc, vc, table, seq_lens = _paged_inputs(B, Hq, Hkv, Sq, lens, D, bs, dtype, seed=sum(lens) + 1, hnd=hnd)
+    print(f"paged single B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} lens={lens} D={D} bs={bs} {dtype} hnd={hnd}", flush=True)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    if hnd:
+        kd, vd = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (kc, vc))
+    args = (q.to(DEV), kd, vd, table.to(DEV), seq_lens.to(DEV), causal)
+    o, lse = paged_attention(*args, max_seq_len=max(lens), return_lse=True)
+    o_split = paged_attention(*args, max_seq_len=max(lens), route="split")
+    torch.cuda.synchronize()
+    _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype)
+    _check(o_split, None, q, kc, vc, table, seq_lens, causal, dtype)
+
+
+def test_paged_single_pass_equals_contiguous_prefill_chunk():
+    """The chunked-prefill BASELINE shape (B=4, 512 new tokens over 8192 keys)
+    from a shuffled 128-key-block cache vs the contiguous single pass."""
+    from gqa_kernels import gqa_flash_attn
+    from gqa_kernels.paged import paged_attention
+    B, Hq, Hkv, Sq, L, D, bs = 4, 32, 8, 512, 8192, 128, 128
+    g = torch.Generator(device=DEV).manual_seed(21)
+    q = torch.randn(B, Hq, Sq, D, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, L, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, L, D, generator=g, device=DEV).to(torch.bfloat16)
+    nper = L // bs
+    perm = torch.randperm(B * nper, generator=g, device=DEV)
+    kc = torch.empty(B * nper, bs, Hkv, D, dtype=torch.bfloat16, device=DEV)
+    vc = torch.empty_like(kc)
+    kc[perm] = k.permute(0, 2, 1, 3).reshape(B * nper, bs, Hkv, D)
+    vc[perm] = v.permute(0, 2, 1, 3).reshape(B * nper, bs, Hkv, D)
+    table = perm.to(torch.int32).view(B, nper)
+    lens = torch.full((B,), L, dtype=torch.int32, device=DEV)
+    o_p = paged_attention(q, kc, vc, table, lens, True)
+    o_c = gqa_flash_attn(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    # same kernel, same tiles in the same order: identical results
+    assert torch.equal(o_p, o_c)
+
+
 @pytest.mark.parametrize("bs,causal", [(16, True), (128, True), (64, False)])
 def test_paged_attention_head_major_cache(bs, causal):
     """Caches stored (num_blocks, Hkv, block_size, D): each head's rows of a

@@ -147,6 +147,43 @@ def test_cache_write_empty_is_noop(lib):
     assert _write(lib, n=0, k=None, v=None, slots=None) == 0
 
 
+def _pfwd(lib, **kw):
+    a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16, lens=_FAKE, bs=64,
+             max_len=1024, o=_FAKE, os=_S4, lse=None, B=2, Hq=32, Hkv=8, Sq=128, D=128, scale=0.1275,
+             causal=1, dtype=0)
+    a.update(kw)
+    return lib.gqa_paged_fwd_launch(a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"], a["tstride"],
+                                    a["lens"], a["bs"], a["max_len"], a["o"], a["os"], a["lse"], a["B"], a["Hq"],
+                                    a["Hkv"], a["Sq"], a["D"], a["scale"], a["causal"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(bs=32), -8), (dict(bs=96), -8), (dict(bs=1 << 17), -8),   # blocks of >= 64 keys, power of two
+    (dict(tstride=15), -8),
+    (dict(lens=None), -7), (dict(table=None), -7), (dict(o=None), -7),
+    (dict(lens=ctypes.c_void_p((1 << 20) + 2)), -4),
+    (dict(lse=ctypes.c_void_p((1 << 20) + 2)), -4),
+    (dict(os=(ctypes.c_int64 * 4)(8 * 128 * 128, 128 * 128, 128, 3)), -4),
+    (dict(D=96), -2), (dict(dtype=9), -3), (dict(Hq=12), -1), (dict(Hq=512, Hkv=1), -6),
+])
+def test_paged_fwd_validation(lib, kw, code):
+    assert _pfwd(lib, **kw) == code
+
+
+def test_paged_fwd_empty_is_noop(lib):
+    assert _pfwd(lib, B=0, q=None, k=None, v=None, table=None, lens=None, o=None) == 0
+    assert _pfwd(lib, Sq=0, q=None, k=None, v=None, table=None, lens=None, o=None) == 0
+
+
+def test_paged_route():
+    from gqa_kernels.paged import paged_route
+    assert paged_route(32, 8, 1, 16) == "split"      # decode
+    assert paged_route(32, 8, 16, 64) == "split"     # 64 packed rows
+    assert paged_route(32, 8, 17, 64) == "single"
+    assert paged_route(32, 8, 512, 16) == "split"    # blocks below one 64-key tile
+    assert paged_route(64, 8, 9, 128) == "single"
+
+
 def test_strerror_block(lib):
     assert b"block_size" in lib.gqa_strerror(-8)
 
