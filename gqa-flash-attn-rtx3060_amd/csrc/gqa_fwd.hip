@@ -412,6 +412,10 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     constexpr int NS = DO_S ? 2 * NKS : 0;
     const char* ck = kstage(s3);
     const char* cv = vstage(s3);
+    // Issue priority: the MFMA-phase wave of a SIMD first (its MFMA stream is
+    // the matrix core's only work), the softmax wave in the gaps (~+2 %).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(3);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 opv[NPV > 0 ? NPV : 1];
     u32x4 opk[NS > 0 ? NS : 1];
@@ -450,6 +454,8 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) pin(acc[db]);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     phase_barrier();
   };
 
@@ -459,6 +465,9 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   // loads it issued one softmax phase earlier.
   auto vphase = [&](auto s3, int tt) {
     constexpr int S3 = decltype(s3)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_sched_barrier(0);
     const int ta = tb + tt;  // absolute tile index
     if (grp == 0) {
       issue_k(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), ta + 2);
@@ -490,6 +499,8 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     pin(l_run);
     pin(m_run);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(ST::NI));  // all but this phase's loads
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     phase_barrier();
   };
 
