@@ -16,7 +16,7 @@ namespace {
 using gqa::Dims;
 using gqa::TensorRef;
 
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -132,6 +132,14 @@ int fwd_impl(const void* q, const int64_t q_stride[4], const void* k, const int6
   return to_code(gqa::launch_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+// Variable query lengths: q_start and q_len both NULL (uniform seq_q) or
+// both 4-byte aligned device arrays.
+int check_varlen(const int* q_start, const int* q_len) {
+  if ((q_start == nullptr) != (q_len == nullptr)) return GQA_E_NULL;
+  if (((reinterpret_cast<uintptr_t>(q_start) | reinterpret_cast<uintptr_t>(q_len)) & 3u) != 0) return GQA_E_STRIDE;
+  return GQA_OK;
+}
+
 int check_lse(const float* lse) {
   if (lse == nullptr) return GQA_E_NULL;
   return (reinterpret_cast<uintptr_t>(lse) & 3u) != 0 ? GQA_E_STRIDE : GQA_OK;
@@ -215,9 +223,10 @@ int gqa_split_first_launch(const void* q, const int64_t q_stride[4], const void*
 int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const void* k_cache,
                                  const int64_t k_cache_stride[4], const void* v_cache,
                                  const int64_t v_cache_stride[4], const int* block_table, int table_stride,
-                                 const int* seq_lens, int block_size, int max_seq_len, float* workspace,
-                                 int splits, int batch, int num_heads, int num_kv_heads, int seq_q, int head_dim,
-                                 float scale_log2, int causal, int dtype, void* stream) {
+                                 const int* seq_lens, const int* q_start, const int* q_len, int block_size,
+                                 int max_seq_len, float* workspace, int splits, int batch, int num_heads,
+                                 int num_kv_heads, int seq_q, int head_dim, float scale_log2, int causal, int dtype,
+                                 void* stream) {
   int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
   if (rc) return rc;
   if (block_size < 1 || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
@@ -228,6 +237,7 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const
   if (workspace == nullptr || seq_lens == nullptr) return GQA_E_NULL;
   if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || (reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0)
     return GQA_E_STRIDE;
+  if ((rc = check_varlen(q_start, q_len))) return rc;
   if ((rc = check_tensor(q, q_stride))) return rc;
   if (max_seq_len > 0) {
     if (block_table == nullptr) return GQA_E_NULL;
@@ -260,13 +270,16 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const
   while ((1 << shift) < block_size) ++shift;
   p.block_shift = shift;
   p.rotate = p.k.ss == head_dim && p.v.ss == head_dim;
+  p.q_start = q_start;
+  p.q_len = q_len;
   return to_code(gqa::launch_paged_split_first(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
 int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4], const void* k_cache,
                          const int64_t k_cache_stride[4], const void* v_cache, const int64_t v_cache_stride[4],
-                         const int* block_table, int table_stride, const int* seq_lens, int block_size,
-                         int max_seq_len, void* o, const int64_t o_stride[4], float* lse, int batch,
+                         const int* block_table, int table_stride, const int* seq_lens, const int* q_start,
+                         const int* q_len, int block_size, int max_seq_len, void* o, const int64_t o_stride[4],
+                         float* lse, int batch,
                          int num_heads, int num_kv_heads, int seq_q, int head_dim, float scale_log2, int causal,
                          int dtype, void* stream) {
   int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
@@ -280,6 +293,7 @@ int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4], const void* k
   if (seq_lens == nullptr) return GQA_E_NULL;
   if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0) return GQA_E_STRIDE;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  if ((rc = check_varlen(q_start, q_len))) return rc;
   if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
   if (max_seq_len > 0) {
     if (block_table == nullptr) return GQA_E_NULL;
@@ -302,6 +316,8 @@ int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4], const void* k
   int shift = 0;
   while ((1 << shift) < block_size) ++shift;
   p.block_shift = shift;
+  p.q_start = q_start;
+  p.q_len = q_len;
   return to_code(gqa::launch_paged_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
@@ -392,7 +408,8 @@ int fused_impl(const void* q, const int64_t q_stride[4], const void* k, const in
 }
 
 int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_stride[4], float* lse, int batch,
-                int num_heads, int seq_q, int head_dim, int dtype, void* stream);
+                int num_heads, int seq_q, int head_dim, int dtype, void* stream, const int* q_start = nullptr,
+                const int* q_len = nullptr);
 
 }  // namespace
 
@@ -431,12 +448,26 @@ int gqa_split_reduce_lse_launch(const float* workspace, int splits, void* o, con
   return reduce_impl(workspace, splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream);
 }
 
+int gqa_split_reduce_varlen_launch(const float* workspace, int splits, void* o, const int64_t o_stride[4],
+                                   float* lse, const int* q_start, const int* q_len, int batch, int num_heads,
+                                   int seq_q, int head_dim, int dtype, void* stream) {
+  if (batch > 0 && seq_q > 0) {
+    int rc = check_varlen(q_start, q_len);
+    if (rc) return rc;
+    if (q_start == nullptr) return GQA_E_NULL;
+    if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  }
+  return reduce_impl(workspace, splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream,
+                     q_start, q_len);
+}
+
 }  // extern "C"
 
 namespace {
 
 int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_stride[4], float* lse, int batch,
-                int num_heads, int seq_q, int head_dim, int dtype, void* stream) {
+                int num_heads, int seq_q, int head_dim, int dtype, void* stream, const int* q_start,
+                const int* q_len) {
   if (batch < 0 || num_heads <= 0 || seq_q < 0) return GQA_E_SHAPE;
   if (head_dim != 64 && head_dim != 128) return GQA_E_HEAD_DIM;
   if (dtype != GQA_DTYPE_BF16 && dtype != GQA_DTYPE_FP16) return GQA_E_DTYPE;
@@ -446,7 +477,7 @@ int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_str
   if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return GQA_E_STRIDE;
   int rc = check_tensor(o, o_stride);
   if (rc) return rc;
-  gqa::ReduceParams p;
+  gqa::ReduceParams p{};
   const size_t rows = (size_t)batch * num_heads * seq_q * splits;
   p.ws_acc = workspace;
   p.ws_m = workspace + rows * head_dim;
@@ -458,6 +489,8 @@ int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_str
   p.D = head_dim;
   p.splits = splits;
   p.lse = lse;
+  p.q_start = q_start;
+  p.q_len = q_len;
   return to_code(gqa::launch_split_reduce(p, dtype, static_cast<hipStream_t>(stream)));
 }
 

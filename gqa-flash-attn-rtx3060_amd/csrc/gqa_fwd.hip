@@ -266,21 +266,29 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
     part = (pid_m >= p.n_mblk - p.n_split) ? 0 : -1;
   }
   const int b = bh / dm.Hkv, kvh = bh - b * dm.Hkv;
-  // Keys of this sequence (paged: its own length, clamped to [0, Skv]).
+  // Keys of this sequence (paged: its own length, clamped to [0, Skv]),
+  // and its query rows (variable lengths: q_len[b], tokens from q_start[b]).
   const int skv = PAGED ? min(max(p.seq_lens[b], 0), dm.Skv) : dm.Skv;
+  const bool varlen = p.q_len != nullptr;
+  const int sq = varlen ? min(max(p.q_len[b], 0), dm.Sq) : dm.Sq;
+  const int64_t tok0 = varlen ? (int64_t)p.q_start[b] : 0;
+  if (pid_m * p.block_m >= sq) return;  // a block past this sequence's queries (variable lengths)
+  // Element offset of (query row pos, head h) in q / o.
+  auto row_off = [&](const TensorRef& t, int pos_, int h) -> int64_t {
+    return varlen ? (tok0 + pos_) * t.ss + (int64_t)h * t.sh : (int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)pos_ * t.ss;
+  };
 
   // This lane's query row.
   const int r = wave * 32 + i;
   const int g = r / p.block_m, ml = r - g * p.block_m;
   const int pos = pid_m * p.block_m + ml;
-  const bool valid = (g < dm.G) && (pos < dm.Sq);
+  const bool valid = (g < dm.G) && (pos < sq);
   const int head = kvh * dm.G + (g < dm.G ? g : 0);
-  const int qpos = pos + (skv - dm.Sq);
+  const int qpos = pos + (skv - sq);
 
   u32x4 qreg[NKS];
   {
-    const T* qrow = static_cast<const T*>(p.q.ptr) + (int64_t)b * p.q.sb + (int64_t)head * p.q.sh +
-                    (int64_t)(valid ? pos : 0) * p.q.ss;
+    const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(p.q, valid ? pos : 0, head);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       u32x4 x = {0u, 0u, 0u, 0u};
@@ -291,16 +299,16 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
 
   // Key range of this workgroup.
   const int pos_lo = pid_m * p.block_m;
-  const int pos_hi = min(pos_lo + p.block_m, dm.Sq) - 1;
+  const int pos_hi = min(pos_lo + p.block_m, sq) - 1;
   int kv_end = skv;
-  if (dm.causal) kv_end = min(skv, pos_hi + (skv - dm.Sq) + 1);
+  if (dm.causal) kv_end = min(skv, pos_hi + (skv - sq) + 1);
   kv_end = max(kv_end, 0);
   const int ntiles_all = (kv_end + ST::kKeys - 1) / ST::kKeys;
   // This item's tiles [tb, tb + ntiles).
   const int tsplit = ntiles_all >> 1;
   const int tb = (part == 1) ? tsplit : 0;
   const int ntiles = (part == 0) ? tsplit : ntiles_all - tb;
-  const int qpos_lo = pos_lo + (skv - dm.Sq);
+  const int qpos_lo = pos_lo + (skv - sq);
 
   // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
   // each ending at the last byte of row seq_kv - 1, and per-lane offsets.
@@ -585,11 +593,13 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
   // to the reference point m_ref); -inf for a row with no visible key.
   const float l_tot = xhalf_sum(l_run);
   const float inv = 1.0f / l_tot;
-  if (p.lse != nullptr && valid && hh == 0)
-    p.lse[((int64_t)b * dm.Hq + head) * dm.Sq + pos] = (m_run * c + __log2f(l_tot)) * kLn2;
+  if (p.lse != nullptr && valid && hh == 0) {
+    // (B, Hq, Sq), or (tokens, Hq) with variable lengths.
+    const int64_t li = varlen ? (tok0 + pos) * dm.Hq + head : ((int64_t)b * dm.Hq + head) * dm.Sq + pos;
+    p.lse[li] = (m_run * c + __log2f(l_tot)) * kLn2;
+  }
   if (valid) {
-    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb +
-              (int64_t)head * p.o.sh + (int64_t)pos * p.o.ss;
+    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(p.o, pos, head);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll

@@ -41,6 +41,12 @@ struct FwdParams {
   const int* seq_lens;
   int table_stride;
   int block_shift;
+  // Variable query lengths (nullptr: every sequence has Sq rows in the
+  // (B, H, S, D) q and o).  Otherwise q and o are token-major: row `pos` of
+  // sequence b, head h is token q_start[b] + pos at ptr + token * ss + h * sh,
+  // and sequence b has q_len[b] <= Sq query rows.
+  const int* q_start;
+  const int* q_len;
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).
@@ -61,13 +67,19 @@ struct SplitParams {
   float* lse;  // optional, fused combine only: as FwdParams::lse
   // Paged K/V cache (gqa_paged_split_first_launch only): k/v point at a
   // (num_blocks, block_size, Hkv, D) cache with sb = block stride, ss = slot
-  // stride, sh = head stride (note: not the dimension order); key j of sequence b is slot j % block_size of
-  // block block_table[b * table_stride + j / block_size]; sequence b has
-  // seq_lens[b] keys (dm.Skv is the longest).
+  // stride, sh = head stride (not the dimension order); key j of sequence b
+  // is slot j % block_size of block block_table[b * table_stride + j /
+  // block_size]; sequence b has seq_lens[b] keys (dm.Skv is the longest).
   const int* block_table;
   const int* seq_lens;
   int table_stride;
   int block_shift;  // log2(block_size)
+  // Variable query lengths (nullptr: every sequence has Sq rows in the
+  // (B, H, S, D) q and o).  Otherwise q and o are token-major: row `pos` of
+  // sequence b, head h is token q_start[b] + pos at ptr + token * ss + h * sh,
+  // and sequence b has q_len[b] <= Sq query rows.
+  const int* q_start;
+  const int* q_len;
   // Stagger the tile order of the splits (set when each head's K and V rows
   // are consecutive: key stride == head_dim).
   int rotate;
@@ -81,6 +93,8 @@ struct ReduceParams {
   TensorRef o;
   int B, Hq, Sq, D, splits;
   float* lse;  // optional: as FwdParams::lse
+  const int* q_start;  // optional: as FwdParams::q_start / q_len
+  const int* q_len;
 };
 
 // Packed query rows per single-pass workgroup (8 waves x 32 rows).

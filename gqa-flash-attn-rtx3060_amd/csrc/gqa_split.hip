@@ -160,18 +160,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // is ever addressed.
   constexpr bool PAGED = KV != 0;
   const int skv = PAGED ? min(max(p.seq_lens[b], 0), dm.Skv) : dm.Skv;
+  // Query rows of this sequence (variable lengths: q_len[b] rows, tokens
+  // from q_start[b]; q token-major).
+  const bool varlen = p.q_len != nullptr;
+  const int sq = varlen ? min(max(p.q_len[b], 0), dm.Sq) : dm.Sq;
+  const int64_t tok0 = varlen ? (int64_t)p.q_start[b] : 0;
+  if ((32 * rb) / dm.G >= sq) return;  // a row block past this sequence's queries
 
   // This lane's query row (position-major packing).
   const int r = 32 * rb + i;
   const int pos = r / dm.G, g = r - pos * dm.G;
-  const bool valid = pos < dm.Sq;
+  const bool valid = pos < sq;
   const int head = kvh * dm.G + g;
-  const int qpos = pos + (skv - dm.Sq);
+  const int qpos = pos + (skv - sq);
 
   u32x4 qreg[D / 16];
   {
-    const T* qrow = static_cast<const T*>(p.q.ptr) + (int64_t)b * p.q.sb + (int64_t)head * p.q.sh +
-                    (int64_t)(valid ? pos : 0) * p.q.ss;
+    const int qp = valid ? pos : 0;
+    const T* qrow = static_cast<const T*>(p.q.ptr) +
+                    (varlen ? (tok0 + qp) * p.q.ss + (int64_t)head * p.q.sh
+                            : (int64_t)b * p.q.sb + (int64_t)head * p.q.sh + (int64_t)qp * p.q.ss);
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       u32x4 x = {0u, 0u, 0u, 0u};
@@ -184,10 +192,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int c0 = s * p.chunk;
   int c1 = min(c0 + p.chunk, skv);
   const int pos_lo = (32 * rb) / dm.G;
-  const int pos_hi = min(dm.Sq - 1, (32 * rb + 31) / dm.G);
-  if (dm.causal) c1 = min(c1, pos_hi + (skv - dm.Sq) + 1);
+  const int pos_hi = min(sq - 1, (32 * rb + 31) / dm.G);
+  if (dm.causal) c1 = min(c1, pos_hi + (skv - sq) + 1);
   const int ntiles = c1 > c0 ? (c1 - c0 + kSplitTileKeys - 1) / kSplitTileKeys : 0;
-  const int qpos_lo = pos_lo + (skv - dm.Sq);
+  const int qpos_lo = pos_lo + (skv - sq);
 
   using Rows = typename std::conditional<PAGED, PagedRows<T, KV == 1>, ContigRows<T>>::type;
   Rows kr, vr;
@@ -368,6 +376,14 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   const int t = threadIdx.x;
   const int row = blockIdx.x;  // ((b * Hq + h) * Sq + pos)
   const int S = p.splits;
+  const int pos = row % p.Sq;
+  const int bh = row / p.Sq;
+  const int h = bh % p.Hq, b = bh / p.Hq;
+  // Variable query lengths: rows past this sequence's queries hold no
+  // partials; o and lse are token-major.
+  const bool varlen = p.q_len != nullptr;
+  if (varlen && pos >= p.q_len[b]) return;
+  const int64_t tok = varlen ? (int64_t)p.q_start[b] + pos : 0;
   const float* wm = p.ws_m + (int64_t)row * S;
   const float* wl = p.ws_l + (int64_t)row * S;
   const float* wa = p.ws_acc + (int64_t)row * S * D;
@@ -402,15 +418,14 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
       o += red_o[k][d4];
       l += red_l[k][d4];
     }
-    const int pos = row % p.Sq;
-    const int bh = row / p.Sq;
-    const int h = bh % p.Hq, b = bh / p.Hq;
     // Optional LSE side output (natural log; m* and l* are log2-domain);
     // -inf for a row with no visible key (whose o stays NaN).
     if (p.lse != nullptr && d4 == 0)
-      p.lse[row] = mstar == -__builtin_inff() ? -__builtin_inff() : (mstar + __log2f(l)) * kLn2;
-    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb + (int64_t)h * p.o.sh +
-              (int64_t)pos * p.o.ss;
+      p.lse[varlen ? tok * p.Hq + h : row] =
+          mstar == -__builtin_inff() ? -__builtin_inff() : (mstar + __log2f(l)) * kLn2;
+    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) +
+              (varlen ? tok * p.o.ss + (int64_t)h * p.o.sh
+                      : (int64_t)b * p.o.sb + (int64_t)h * p.o.sh + (int64_t)pos * p.o.ss);
     u32x2 x;
     x[0] = E::pack2(o[0] / l, o[1] / l);
     x[1] = E::pack2(o[2] / l, o[3] / l);

@@ -18,7 +18,7 @@ DTYPE_FP16 = 1
 
 GQA_MAX_SPLITS = 1024
 GQA_MAX_BLOCK_SIZE = 65536
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -66,12 +66,13 @@ SIGNATURES = {
     ),
     "gqa_paged_split_first_launch": (
         _i,
-        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _i, _i, _p, _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _p, _p, _i, _i, _p, _i,
          _i, _i, _i, _i, _i, _f, _i, _i, _p],
     ),
+    "gqa_split_reduce_varlen_launch": (_i, [_p, _i, _p, _i64x4, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
     "gqa_paged_fwd_launch": (
         _i,
-        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _i, _i, _p, _i64x4, _p,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _p, _p, _i, _i, _p, _i64x4, _p,
          _i, _i, _i, _i, _i, _f, _i, _i, _p],
     ),
     "gqa_paged_cache_write_launch": (

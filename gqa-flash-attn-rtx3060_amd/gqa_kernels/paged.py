@@ -119,7 +119,9 @@ def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int) 
 def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
                     max_seq_len: Optional[int] = None, scale: Optional[float] = None,
                     splits: Optional[int] = None, return_lse: bool = False,
-                    out: Optional[torch.Tensor] = None, route: Optional[str] = None):
+                    out: Optional[torch.Tensor] = None, route: Optional[str] = None,
+                    query_start: Optional[torch.Tensor] = None, query_lens: Optional[torch.Tensor] = None,
+                    max_query_len: Optional[int] = None):
     """GQA attention of q over K/V held in a paged cache.
 
     Args:
@@ -146,11 +148,29 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             (any strides with 16-byte aligned rows) to write o into.
         route: "split" or "single" to force a kernel (default: paged_route;
             "single" needs block_size >= 64).
+        query_start, query_lens, max_query_len: variable query lengths.  q
+            is then token-major (num_tokens, num_heads, head_dim); sequence
+            b's queries are tokens query_start[b] .. + query_lens[b] - 1
+            (int32 device tensors of batch entries), max_query_len (a host
+            int) bounds query_lens; causal alignment per sequence uses its own
+            query length; o (and out) are (num_tokens, num_heads, head_dim),
+            lse (num_tokens, num_heads).
 
     Returns:
         o (batch, num_heads, seq_q, head_dim), or (o, lse).
     """
-    batch, num_heads, seq_q, head_dim = q.shape
+    varlen = query_start is not None
+    if varlen:
+        assert query_lens is not None and max_query_len is not None, "varlen needs query_lens and max_query_len"
+        assert q.dim() == 3, "varlen q is (num_tokens, num_heads, head_dim)"
+        num_tokens, num_heads, head_dim = q.shape
+        batch, seq_q = seq_lens.shape[0], int(max_query_len)
+        assert query_start.dtype == torch.int32 and query_lens.dtype == torch.int32
+        assert tuple(query_start.shape) == (batch,) and tuple(query_lens.shape) == (batch,)
+        assert query_start.device == q.device and query_lens.device == q.device
+        query_start, query_lens = query_start.contiguous(), query_lens.contiguous()
+    else:
+        batch, num_heads, seq_q, head_dim = q.shape
     block_size = _check_cache(k_cache, v_cache)
     num_kv_heads = k_cache.shape[2]
     assert num_heads % num_kv_heads == 0, "num_heads must be divisible by num_kv_heads"
@@ -166,6 +186,9 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     seq_lens = seq_lens.contiguous()
     if not _rows_ready(q):
         q = q.contiguous()
+    if varlen:
+        # one 16-byte aligned token row per head
+        assert q.stride(2) == 1 and (q.stride(1) * q.element_size()) % 16 == 0
 
     table_stride = block_table.stride(0) if batch > 1 else block_table.shape[1]
     capacity = block_table.shape[1] * block_size
@@ -179,39 +202,48 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
         scale = head_dim ** -0.5
 
     if out is None:
-        out = torch.empty(batch, num_heads, seq_q, head_dim, dtype=q.dtype, device=q.device)
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     else:
         assert tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype and out.device == q.device
         assert _rows_ready(out), "out rows must be contiguous and 16-byte aligned"
+    # Token-major q / o as the kernels address them: (unused, head, token, d).
+    qst = _lib._i64x4(0, q.stride(1), q.stride(0), 1) if varlen else _lib.strides(q)
+    ost = _lib._i64x4(0, out.stride(1), out.stride(0), 1) if varlen else _lib.strides(out)
+    qs_p = query_start.data_ptr() if varlen else None
+    ql_p = query_lens.data_ptr() if varlen else None
+    lse_shape = (q.shape[0], num_heads) if varlen else (batch, num_heads, seq_q)
 
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
     stream = torch.cuda.current_stream(q.device).cuda_stream
     route = route or paged_route(num_heads, num_kv_heads, seq_q, block_size)
     assert route in ("split", "single") and (route == "split" or block_size >= 64)
+    lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if return_lse else None
+    lse_p = None if lse is None else lse.data_ptr()
     if route == "single":
-        lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
         _lib.check(lib.gqa_paged_fwd_launch(
-            q.data_ptr(), _lib.strides(q), k_cache.data_ptr(), _lib.strides(k_cache),
+            q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),
             v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
-            seq_lens.data_ptr(), block_size, max_seq_len, out.data_ptr(), _lib.strides(out),
-            None if lse is None else lse.data_ptr(), batch, num_heads, num_kv_heads, seq_q, head_dim,
+            seq_lens.data_ptr(), qs_p, ql_p, block_size, max_seq_len, out.data_ptr(), ost,
+            lse_p, batch, num_heads, num_kv_heads, seq_q, head_dim,
             scale * LOG2E, int(bool(causal)), dtype, stream))
         return out if lse is None else (out, lse)
     workspace = _workspace_buffer(q.device, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, splits))
     _lib.check(lib.gqa_paged_split_first_launch(
-        q.data_ptr(), _lib.strides(q), k_cache.data_ptr(), _lib.strides(k_cache),
+        q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),
         v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
-        seq_lens.data_ptr(), block_size, max_seq_len, workspace.data_ptr(), splits,
+        seq_lens.data_ptr(), qs_p, ql_p, block_size, max_seq_len, workspace.data_ptr(), splits,
         batch, num_heads, num_kv_heads, seq_q, head_dim, scale * LOG2E, int(bool(causal)), dtype, stream))
-    if not return_lse:
-        _lib.check(lib.gqa_split_reduce_launch(workspace.data_ptr(), splits, out.data_ptr(), _lib.strides(out),
+    if varlen:
+        _lib.check(lib.gqa_split_reduce_varlen_launch(workspace.data_ptr(), splits, out.data_ptr(), ost, lse_p,
+                                                      qs_p, ql_p, batch, num_heads, seq_q, head_dim, dtype, stream))
+    elif lse is None:
+        _lib.check(lib.gqa_split_reduce_launch(workspace.data_ptr(), splits, out.data_ptr(), ost,
                                                batch, num_heads, seq_q, head_dim, dtype, stream))
-        return out
-    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device)
-    _lib.check(lib.gqa_split_reduce_lse_launch(workspace.data_ptr(), splits, out.data_ptr(), _lib.strides(out),
-                                               lse.data_ptr(), batch, num_heads, seq_q, head_dim, dtype, stream))
-    return out, lse
+    else:
+        _lib.check(lib.gqa_split_reduce_lse_launch(workspace.data_ptr(), splits, out.data_ptr(), ost,
+                                                   lse_p, batch, num_heads, seq_q, head_dim, dtype, stream))
+    return out if lse is None else (out, lse)
 
 
 def write_kv(key, value, k_cache, v_cache, slot_mapping):
@@ -404,8 +436,10 @@ class PagedAttentionMetadata:
     slot_mapping: int64 (num_tokens,) cache slot of every new token (-1: pad).
     block_tables: int32 (num_seqs, max_blocks_per_seq).
     seq_lens: int32 (num_seqs,) keys per sequence, new tokens included.
-    query_len: new tokens per sequence (the same for every sequence: 1 for
+    query_len: new tokens per sequence when they are all equal (1 for
         decode, k for speculative verification, the chunk for chunked prefill).
+    query_lens: new tokens of each sequence (host ints) for a mixed batch
+        (prefill chunks and decode steps together); overrides query_len.
     max_seq_len: an upper bound of seq_lens (default: the tables' capacity).
     """
     slot_mapping: torch.Tensor
@@ -413,6 +447,7 @@ class PagedAttentionMetadata:
     seq_lens: torch.Tensor
     query_len: int = 1
     max_seq_len: Optional[int] = None
+    query_lens: Optional[Sequence[int]] = None
 
 
 class GQAPagedAttention(torch.nn.Module):
@@ -422,11 +457,14 @@ class GQAPagedAttention(torch.nn.Module):
       query (num_tokens, num_heads * head_size), key/value
       (num_tokens, num_kv_heads * head_size) or None (nothing to store),
       kv_cache (2, num_blocks, block_size, num_kv_heads, head_size).
-    Tokens are sequence-major, ``attn_metadata.query_len`` per sequence.  The
-    new K/V are stored at ``slot_mapping`` first, then every query attends its
-    sequence's cache (causal, bottom-right aligned).  Returns
-    (num_tokens, num_heads * head_size), written in place when ``output`` is
-    given.
+    Tokens are sequence-major: ``attn_metadata.query_len`` per sequence, or
+    ``attn_metadata.query_lens[b]`` for sequence b of a mixed batch.  The new
+    K/V are stored at ``slot_mapping`` first, then every query attends its
+    sequence's cache (causal, bottom-right aligned).  A mixed batch runs as
+    up to two launches over token-major q/o views, one for the sequences
+    whose query block suits the split-KV pass (decode-like) and one for the
+    rest (prefill chunks).  Returns (num_tokens, num_heads * head_size),
+    written in place when ``output`` is given.
     """
 
     def __init__(self, num_heads: int, head_size: int, scale: Optional[float] = None,
@@ -444,18 +482,41 @@ class GQAPagedAttention(torch.nn.Module):
         md = attn_metadata
         num_tokens = query.shape[0]
         H, Hkv, D = self.num_heads, self.num_kv_heads, self.head_size
-        sq = md.query_len
         batch = md.block_tables.shape[0]
-        assert num_tokens == batch * sq, "num_tokens must equal num_seqs * query_len"
         assert kv_cache.dim() == 5 and kv_cache.shape[0] == 2 and kv_cache.shape[3] == Hkv and kv_cache.shape[4] == D
         k_cache, v_cache = kv_cache[0], kv_cache[1]
+        if md.query_lens is None:
+            assert num_tokens == batch * md.query_len, "num_tokens must equal num_seqs * query_len"
+        else:
+            assert len(md.query_lens) == batch and sum(md.query_lens) == num_tokens
         if key is not None:
             write_kv(key.view(num_tokens, Hkv, D), value.view(num_tokens, Hkv, D), k_cache, v_cache,
                      md.slot_mapping)
         if output is None:
             output = torch.empty(num_tokens, H * D, dtype=query.dtype, device=query.device)
-        q4 = query.view(batch, sq, H, D).permute(0, 2, 1, 3)
-        o4 = output.view(batch, sq, H, D).permute(0, 2, 1, 3)
-        paged_attention(q4, k_cache, v_cache, md.block_tables, md.seq_lens, self.causal,
-                        max_seq_len=md.max_seq_len, scale=self.scale, out=o4)
+        if md.query_lens is None:
+            sq = md.query_len
+            q4 = query.view(batch, sq, H, D).permute(0, 2, 1, 3)
+            o4 = output.view(batch, sq, H, D).permute(0, 2, 1, 3)
+            paged_attention(q4, k_cache, v_cache, md.block_tables, md.seq_lens, self.causal,
+                            max_seq_len=md.max_seq_len, scale=self.scale, out=o4)
+            return output
+        # Mixed batch: token-major views, one launch per kernel route.
+        q3, o3 = query.view(num_tokens, H, D), output.view(num_tokens, H, D)
+        starts = [0] * batch
+        for b in range(1, batch):
+            starts[b] = starts[b - 1] + md.query_lens[b - 1]
+        groups: Dict[str, List[int]] = {}
+        for b, ql in enumerate(md.query_lens):
+            if ql > 0:
+                groups.setdefault(paged_route(H, Hkv, ql, k_cache.shape[1]), []).append(b)
+        dev = query.device
+        for route, idx in groups.items():
+            sel = torch.tensor(idx, dtype=torch.int64).to(dev)
+            qs = torch.tensor([starts[b] for b in idx], dtype=torch.int32).to(dev)
+            ql = torch.tensor([md.query_lens[b] for b in idx], dtype=torch.int32).to(dev)
+            paged_attention(q3, k_cache, v_cache, md.block_tables.index_select(0, sel),
+                            md.seq_lens.index_select(0, sel), self.causal, max_seq_len=md.max_seq_len,
+                            scale=self.scale, out=o3, route=route, query_start=qs, query_lens=ql,
+                            max_query_len=max(md.query_lens[b] for b in idx))
         return output

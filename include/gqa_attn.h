@@ -196,11 +196,21 @@ int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4],
  * block_size a power of two.  Key j of sequence b is slot j % block_size of
  * block block_table[b * table_stride + j / block_size]; sequence b has
  * seq_lens[b] keys.  block_table and seq_lens are int32 device arrays.
- * Sequences may share blocks (a common prefix stored once). */
+ * Sequences may share blocks (a common prefix stored once).
+ *
+ * Variable query lengths (q_start and q_len, both NULL or both int32 device
+ * arrays of batch entries): q and o are then token-major — row pos of
+ * sequence b and head h is token q_start[b] + pos, at element offset
+ * token * stride[2] + h * stride[1] (stride[0] is not used) — and sequence b
+ * has q_len[b] <= seq_q query rows; causal alignment uses its own
+ * q_len[b]: query row i attends keys [0, i + seq_lens[b] - q_len[b]].
+ * Rows past q_len[b] are neither read nor written, and an LSE side output is
+ * (tokens, num_heads).  With both NULL, q and o are (batch, num_heads,
+ * seq_q, head_dim) as everywhere else. */
 
 /* Split-KV first pass over a paged cache; combine with
  * gqa_split_reduce_launch / gqa_split_reduce_lse_launch (same workspace
- * layout).  q is (batch, num_heads, seq_q, head_dim) as above; with causal,
+ * layout), or gqa_split_reduce_varlen_launch with variable query lengths.  q is (batch, num_heads, seq_q, head_dim) as above; with causal,
  * query row i of sequence b attends keys [0, i + seq_lens[b] - seq_q]
  * (the bottom-right alignment of the contiguous path, per sequence).
  * max_seq_len bounds the sequences (seq_lens[b] is clamped to
@@ -212,7 +222,8 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4],
                                  const void* k_cache, const int64_t k_cache_stride[4],
                                  const void* v_cache, const int64_t v_cache_stride[4],
                                  const int* block_table, int table_stride,
-                                 const int* seq_lens, int block_size, int max_seq_len,
+                                 const int* seq_lens, const int* q_start, const int* q_len,
+                                 int block_size, int max_seq_len,
                                  float* workspace, int splits,
                                  int batch, int num_heads, int num_kv_heads,
                                  int seq_q, int head_dim,
@@ -230,11 +241,21 @@ int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4],
                          const void* k_cache, const int64_t k_cache_stride[4],
                          const void* v_cache, const int64_t v_cache_stride[4],
                          const int* block_table, int table_stride,
-                         const int* seq_lens, int block_size, int max_seq_len,
+                         const int* seq_lens, const int* q_start, const int* q_len,
+                         int block_size, int max_seq_len,
                          void* o, const int64_t o_stride[4], float* lse,
                          int batch, int num_heads, int num_kv_heads,
                          int seq_q, int head_dim,
                          float scale_log2, int causal, int dtype, void* stream);
+
+/* gqa_split_reduce_launch for variable query lengths (q_start, q_len as
+ * above, non-NULL; o token-major); lse may be NULL or receives (tokens,
+ * num_heads). */
+int gqa_split_reduce_varlen_launch(const float* workspace, int splits,
+                                   void* o, const int64_t o_stride[4], float* lse,
+                                   const int* q_start, const int* q_len,
+                                   int batch, int num_heads, int seq_q, int head_dim,
+                                   int dtype, void* stream);
 
 /* Store new tokens' K and V into the paged caches:
  * k_cache[slot / block_size, slot % block_size, h, :] = k[t, h, :] (and V)

@@ -292,3 +292,82 @@ def test_vllm_shaped_layer_decode_and_chunk(layout):
                                        np.array([L]), True)
             got = to_np(out[s * sq:(s + 1) * sq].view(sq, Hq, D).permute(1, 0, 2)[None])
             assert_close(got, ref_o, BASELINE_TOL[dt], f"layer seq {s} sq {sq}")
+
+
+def _varlen_inputs(Hq, Hkv, D, lens, qlens, bs, dtype, seed):
+    """Paged cache as _paged_inputs and a token-major q of sum(qlens) rows."""
+    _, kc, vc, table, seq_lens = _paged_inputs(len(lens), Hq, Hkv, 1, lens, D, bs, dtype, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    q = torch.randn(sum(qlens), Hq, D, generator=g).to(dtype)
+    starts = [sum(qlens[:b]) for b in range(len(qlens))]
+    return q, kc, vc, table, seq_lens, starts
+
+
+def _check_varlen(o, lse, q, kc, vc, table, seq_lens, starts, qlens, causal, dtype):
+    for b, (s0, n) in enumerate(zip(starts, qlens)):
+        if n == 0:
+            continue
+        qb = q[s0:s0 + n].permute(1, 0, 2)[None]  # (1, Hq, n, D)
+        ob = o[s0:s0 + n].permute(1, 0, 2)[None]
+        lb = None if lse is None else lse[s0:s0 + n].t()[None]
+        _check(ob, lb, qb, kc, vc, table[b:b + 1], seq_lens[b:b + 1], causal, dtype)
+
+
+@pytest.mark.parametrize("route,bs,causal", [("single", 64, True), ("split", 64, True), ("split", 16, True),
+                                             ("single", 128, False)])
+def test_paged_variable_query_lengths(route, bs, causal):
+    from gqa_kernels.paged import paged_attention
+    Hq, Hkv, D = 32, 8, 128
+    lens = [900, 40, 2000, 130, 7]
+    qlens = [1, 37, 5, 130, 7]  # a decode step, chunks, a whole short sequence
+    dt = torch.bfloat16
+    q, kc, vc, table, seq_lens, starts = _varlen_inputs(Hq, Hkv, D, lens, qlens, bs, dt, seed=31 + bs)
+    print(f"varlen route={route} bs={bs} causal={causal}", flush=True)
+    qs = torch.tensor(starts, dtype=torch.int32, device=DEV)
+    ql = torch.tensor(qlens, dtype=torch.int32, device=DEV)
+    o, lse = paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), causal,
+                             max_seq_len=max(lens), return_lse=True, route=route, query_start=qs, query_lens=ql,
+                             max_query_len=max(qlens))
+    torch.cuda.synchronize()
+    assert tuple(o.shape) == tuple(q.shape) and tuple(lse.shape) == (q.shape[0], Hq)
+    _check_varlen(o.cpu(), lse.cpu(), q, kc, vc, table, seq_lens, starts, qlens, causal, dt)
+
+
+def test_vllm_shaped_layer_mixed_batch():
+    """Prefill chunks and decode steps in one call: the layer runs one launch
+    per kernel route over token-major views."""
+    from gqa_kernels.paged import GQAPagedAttention, PagedAttentionMetadata, PagedKVCache
+    Hq, Hkv, D, bs = 32, 8, 128, 64
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(17)
+    cache = PagedKVCache(300, bs, Hkv, D, dtype=dt, device=DEV)
+    layer = GQAPagedAttention(Hq, D, num_kv_heads=Hkv)
+    hist = {}
+    for s, n in enumerate([1200, 0, 3000, 55]):  # sequence 1 starts empty (a fresh prompt)
+        cache.add_sequence(s)
+        k = torch.randn(n, Hkv, D, generator=g).to(dt)
+        v = torch.randn(n, Hkv, D, generator=g).to(dt)
+        if n:
+            cache.append([s], k.to(DEV), v.to(DEV))
+        hist[s] = (k, v)
+    qlens = [1, 200, 1, 30]  # decode, a whole prompt, decode, a chunk
+    T = sum(qlens)
+    query = torch.randn(T, Hq * D, generator=g).to(dt)
+    key = torch.randn(T, Hkv * D, generator=g).to(dt)
+    value = torch.randn(T, Hkv * D, generator=g).to(dt)
+    slots = torch.tensor(sum((cache.reserve(s, n) for s, n in enumerate(qlens)), []), dtype=torch.int64)
+    md = PagedAttentionMetadata(slot_mapping=slots.to(DEV), block_tables=cache.block_table(range(4)),
+                                seq_lens=cache.seq_lens(range(4)), query_lens=qlens)
+    out = layer(query.to(DEV), key.to(DEV), value.to(DEV), cache.kv, md)
+    torch.cuda.synchronize()
+    t0 = 0
+    for s, n in enumerate(qlens):
+        k, v = hist[s]
+        k = torch.cat([k, key[t0:t0 + n].view(n, Hkv, D)])
+        v = torch.cat([v, value[t0:t0 + n].view(n, Hkv, D)])
+        L = k.shape[0]
+        q4 = to_np(query[t0:t0 + n].view(n, Hq, D).permute(1, 0, 2)[None])
+        ref_o, _ = paged_reference(q4, to_np(k[:, None]), to_np(v[:, None]), np.arange(L)[None], np.array([L]), True)
+        got = to_np(out[t0:t0 + n].view(n, Hq, D).permute(1, 0, 2)[None])
+        assert_close(got, ref_o, BASELINE_TOL[dt], f"mixed batch seq {s}")
+        t0 += n

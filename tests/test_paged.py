@@ -91,13 +91,13 @@ _FAKE = ctypes.c_void_p(1 << 20)
 
 def _paged(lib, **kw):
     a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16,
-             lens=_FAKE, bs=64, max_len=1024, ws=_FAKE, splits=8, B=2, Hq=32, Hkv=8, Sq=1, D=128,
-             scale=0.1275, causal=1, dtype=0)
+             lens=_FAKE, qstart=None, qlen=None, bs=64, max_len=1024, ws=_FAKE, splits=8, B=2, Hq=32, Hkv=8,
+             Sq=1, D=128, scale=0.1275, causal=1, dtype=0)
     a.update(kw)
     return lib.gqa_paged_split_first_launch(
-        a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"], a["tstride"], a["lens"], a["bs"],
-        a["max_len"], a["ws"], a["splits"], a["B"], a["Hq"], a["Hkv"], a["Sq"], a["D"], a["scale"],
-        a["causal"], a["dtype"], None)
+        a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"], a["tstride"], a["lens"], a["qstart"],
+        a["qlen"], a["bs"], a["max_len"], a["ws"], a["splits"], a["B"], a["Hq"], a["Hkv"], a["Sq"], a["D"],
+        a["scale"], a["causal"], a["dtype"], None)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -110,6 +110,8 @@ def _paged(lib, **kw):
     (dict(ws=ctypes.c_void_p((1 << 20) + 4)), -4),
     (dict(ks=(ctypes.c_int64 * 4)(64 * 8 * 128, 8 * 128, 128, 2)), -4),
     (dict(D=96), -2), (dict(dtype=5), -3), (dict(Hq=30), -1), (dict(max_len=-1), -1),
+    (dict(qstart=_FAKE), -7), (dict(qlen=_FAKE), -7),                # variable lengths need both
+    (dict(qstart=_FAKE, qlen=ctypes.c_void_p((1 << 20) + 2)), -4),
 ])
 def test_paged_first_validation(lib, kw, code):
     assert _paged(lib, **kw) == code
@@ -148,13 +150,14 @@ def test_cache_write_empty_is_noop(lib):
 
 
 def _pfwd(lib, **kw):
-    a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16, lens=_FAKE, bs=64,
-             max_len=1024, o=_FAKE, os=_S4, lse=None, B=2, Hq=32, Hkv=8, Sq=128, D=128, scale=0.1275,
-             causal=1, dtype=0)
+    a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16, lens=_FAKE,
+             qstart=None, qlen=None, bs=64, max_len=1024, o=_FAKE, os=_S4, lse=None, B=2, Hq=32, Hkv=8, Sq=128,
+             D=128, scale=0.1275, causal=1, dtype=0)
     a.update(kw)
     return lib.gqa_paged_fwd_launch(a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"], a["tstride"],
-                                    a["lens"], a["bs"], a["max_len"], a["o"], a["os"], a["lse"], a["B"], a["Hq"],
-                                    a["Hkv"], a["Sq"], a["D"], a["scale"], a["causal"], a["dtype"], None)
+                                    a["lens"], a["qstart"], a["qlen"], a["bs"], a["max_len"], a["o"], a["os"],
+                                    a["lse"], a["B"], a["Hq"], a["Hkv"], a["Sq"], a["D"], a["scale"], a["causal"],
+                                    a["dtype"], None)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -165,6 +168,8 @@ def _pfwd(lib, **kw):
     (dict(lse=ctypes.c_void_p((1 << 20) + 2)), -4),
     (dict(os=(ctypes.c_int64 * 4)(8 * 128 * 128, 128 * 128, 128, 3)), -4),
     (dict(D=96), -2), (dict(dtype=9), -3), (dict(Hq=12), -1), (dict(Hq=512, Hkv=1), -6),
+    (dict(qstart=_FAKE), -7), (dict(qlen=_FAKE), -7),
+    (dict(qstart=ctypes.c_void_p((1 << 20) + 1), qlen=_FAKE), -4),
 ])
 def test_paged_fwd_validation(lib, kw, code):
     assert _pfwd(lib, **kw) == code
@@ -173,6 +178,15 @@ def test_paged_fwd_validation(lib, kw, code):
 def test_paged_fwd_empty_is_noop(lib):
     assert _pfwd(lib, B=0, q=None, k=None, v=None, table=None, lens=None, o=None) == 0
     assert _pfwd(lib, Sq=0, q=None, k=None, v=None, table=None, lens=None, o=None) == 0
+
+
+def test_reduce_varlen_validation(lib):
+    r = lib.gqa_split_reduce_varlen_launch
+    assert r(_FAKE, 8, _FAKE, _S4, None, None, None, 2, 32, 16, 128, 0, None) == -7
+    assert r(_FAKE, 8, _FAKE, _S4, None, _FAKE, None, 2, 32, 16, 128, 0, None) == -7
+    assert r(_FAKE, 8, _FAKE, _S4, ctypes.c_void_p((1 << 20) + 2), _FAKE, _FAKE, 2, 32, 16, 128, 0, None) == -4
+    assert r(_FAKE, 0, _FAKE, _S4, None, _FAKE, _FAKE, 2, 32, 16, 128, 0, None) == -5
+    assert r(None, 8, None, _S4, None, None, None, 0, 32, 16, 128, 0, None) == 0  # empty batch
 
 
 def test_paged_route():
