@@ -242,10 +242,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
     ap.add_argument("--sweep", action="store_true", help="also time every BASELINE config")
-    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b"],
+                    default=None,
                     help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
                          "device copy, the calibration kernel of the HBM traffic counters; 'gemm' "
-                         "a 16384^3 bf16 library GEMM, the practical MFMA ceiling of the box")
+                         "a 16384^3 bf16 library GEMM, the practical MFMA ceiling of the box; "
+                         "'chunked' and '70b' one BASELINE config of the sweep each")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -347,6 +349,8 @@ def main() -> int:
 
     if args.sweep:
         result["sweep"] = sweep(torch, gqa_flash_attn)
+    if args.only in ("chunked", "70b"):
+        result["sweep"] = sweep(torch, gqa_flash_attn, only=args.only)
 
     if result["value"] is None and "decode" in result:
         d = result["decode"]
@@ -414,11 +418,14 @@ def paged_prefill(torch, steps, warmup):
     return out
 
 
-def sweep(torch, gqa_flash_attn):
-    """Every BASELINE config: mean ms over 20 calls after 5 warm-ups."""
+def sweep(torch, gqa_flash_attn, only=None):
+    """Every BASELINE config (or the one named `only`): mean ms over 20 calls
+    after 5 warm-ups."""
     cfgs = [("prefill", 1, 32, 8, s, s) for s in (2048, 4096, 8192, 16384)]
     cfgs += [("decode", 1, 32, 8, 1, s) for s in (8192, 32768, 131072)]
     cfgs += [("chunked", 4, 32, 8, 512, 8192), ("70b", 16, 64, 8, 4, 32768)]
+    if only is not None:
+        cfgs = [c for c in cfgs if c[0] == only]
     rows = []
     for name, b, hq, hkv, sq, skv in cfgs:
         by1 = hbm_bytes(b, hq, hkv, sq, skv, D)
