@@ -137,22 +137,28 @@ __device__ inline float vmax3(float a, float b, float c) {
 // per lane and block; the two lane halves hold the other 16 keys of the
 // same row), exp2 domain.
 //
-// Lazy rescaling: the reference point m_ref of a row is only raised when the
-// tile's max exceeds it by more than kRescaleLog2 (log2 units); otherwise the
-// probabilities are computed against the stale m_ref and may reach
-// 2^kRescaleLog2, which bf16/fp16 P and fp32 l/acc hold exactly as well.  The
-// decision is wave-uniform, so in steady state the O accumulators are not
-// touched by the VALU at all.  The result o = acc / l is unchanged (both are
-// relative to the same m_ref).  A row whose m_ref is still -inf uses 0 as the
+// Lazy rescaling: the reference point m_ref of a row is kept as long as the
+// probabilities computed against it stay at most 2^kRescaleLog2, which
+// bf16/fp16 P and fp32 l/acc hold as exactly as probabilities <= 1.  A tile's
+// exponentials are first computed against the current m_ref, with no row
+// max; a lane's partial row sum bounds each of its probabilities, so only
+// when some lane's sum exceeds 2^kRescaleLog2 (or is NaN / inf), or some row
+// has no reference yet, does the wave take the tile's exact row max, raise
+// m_ref to it, rescale l and the accumulators, and recompute the tile's
+// exponentials.  The decision is wave-uniform, so in steady state neither a
+// max tree nor the O accumulators cost VALU work.  The result o = acc / l is
+// unchanged (both are relative to the same m_ref).  A row whose m_ref is
+// still -inf after the exact pass (every key masked so far) uses 0 as the
 // reference, so a fully masked tile contributes p = 0, never NaN.
 // ---------------------------------------------------------------------------
 constexpr float kRescaleLog2 = 8.0f;
+constexpr float kRescaleSum = 256.0f;  // 2^kRescaleLog2
 
-// Tile row max (a max3 tree), and the rare rescale of l and the
-// accumulators.  Returns -m_ref * c, the offset of the exponent.
+// Exact pass: the tile's row max (a max3 tree), m_ref raised to it, l and the
+// accumulators rescaled.  Returns -m_ref * c, the offset of the exponent.
 template <int NACC>
-__device__ inline float softmax_rescale(const f32x16 (&s)[2], float& m_ref, float& l_run, f32x16 (&acc)[NACC],
-                                        float c) {
+__device__ inline float softmax_rebase(const f32x16 (&s)[2], float& m_ref, float& l_run, f32x16 (&acc)[NACC],
+                                       float c) {
   float m1[11];
 #pragma unroll
   for (int k = 0; k < 10; ++k) {
@@ -163,19 +169,16 @@ __device__ inline float softmax_rescale(const f32x16 (&s)[2], float& m_ref, floa
   const float n0 = vmax3(m1[0], m1[1], m1[2]), n1 = vmax3(m1[3], m1[4], m1[5]);
   const float n2 = vmax3(m1[6], m1[7], m1[8]), n3 = vmax3(m1[9], m1[10], m1[10]);
   const float mx = xhalf_max(vmax3(vmax3(n0, n1, n2), n3, n3));
-  const bool grow = (mx - m_ref) * c > kRescaleLog2;  // false for NaN (both -inf)
-  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-    const float m_new = fmaxf(m_ref, mx);
-    const float m_new_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = fast_exp2((m_ref - m_new_use) * c);
-    l_run *= alpha;
+  const float m_new = fmaxf(m_ref, mx);
+  const float m_new_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+  const float alpha = fast_exp2((m_ref - m_new_use) * c);
+  l_run *= alpha;
 #pragma unroll
-    for (int db = 0; db < NACC; ++db)
+  for (int db = 0; db < NACC; ++db)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
-    m_ref = m_new;
-  }
-  return -((m_ref == -__builtin_inff()) ? 0.f : m_ref) * c;
+    for (int v = 0; v < 16; ++v) acc[db][v] *= alpha;
+  m_ref = m_new;
+  return -m_new_use * c;
 }
 
 // One 32-key block: p = 2^(s*c - m_ref*c) in fp32, rounded to the input type
@@ -220,15 +223,18 @@ __device__ __forceinline__ void mphase_pipe() {
 
 // PAGED: K/V tiles come from a paged cache through the block table (one
 // buffer descriptor per 64-key tile, ending at the sequence's last key).
+// D = 64 keeps to 128 VGPRs (four waves per SIMD): two workgroups share a
+// compute unit, which outweighs the shorter LDS-read lookahead it needs.
 template <int DT, int D, bool PAGED>
-__global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void gqa_fwd_kernel(
+    FwdParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
   using ST = FwdStage<D>;
   constexpr int CPR = ST::CPR;
   constexpr int NDB = D / 32;  // 32-wide d blocks of O^T
   constexpr int NKS = D / 16;  // k-steps of S^T
-  constexpr int PF = 6;        // MFMA slots of LDS-read lookahead
+  constexpr int PF = (D == 64) ? 4 : 6;  // MFMA slots of LDS-read lookahead
   // Six separate arrays (not one): the compiler can then tell the LDS-DMA
   // targets of later tiles from the buffers being read, and does not wait for
   // those loads before the reads.
@@ -494,9 +500,22 @@ __global__ __launch_bounds__(512) void gqa_fwd_kernel(FwdParams p) {
           sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
     }
-    const float nmc = softmax_rescale<NDB>(sc, m_run, l_run, acc, c);
-    const float rs0 = softmax_exp<DT>(sc[0], nmc, c, pk[0]);
-    const float rs1 = softmax_exp<DT>(sc[1], nmc, c, pk[1]);
+    // Exponentials against the current reference; the exact pass when a
+    // row has none yet or a lane's partial sum leaves the bound (not
+    // `> kRescaleSum`: NaN and inf sums take the exact pass too).
+    float rs0 = 0.f, rs1 = 0.f;
+    bool keep = __builtin_amdgcn_ballot_w64(m_run == -__builtin_inff()) == 0;
+    if (keep) {
+      const float nmc = -m_run * c;
+      rs0 = softmax_exp<DT>(sc[0], nmc, c, pk[0]);
+      rs1 = softmax_exp<DT>(sc[1], nmc, c, pk[1]);
+      keep = __builtin_amdgcn_ballot_w64(!(rs0 + rs1 <= kRescaleSum)) == 0;
+    }
+    if (!keep) {
+      const float nmc = softmax_rebase<NDB>(sc, m_run, l_run, acc, c);
+      rs0 = softmax_exp<DT>(sc[0], nmc, c, pk[0]);
+      rs1 = softmax_exp<DT>(sc[1], nmc, c, pk[1]);
+    }
     l_run += rs0 + rs1;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)

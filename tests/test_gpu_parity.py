@@ -308,6 +308,33 @@ def test_fully_masked_rows_are_nan():
     assert_close(out[:, :, 16:], ref[:, :, 16:], BASELINE_TOL[torch.bfloat16], "masked")
 
 
+# --------------------------------------------------------------------------
+# Online-softmax reference points: scores that grow along the keys (later
+# tiles exceed the running reference, so it is raised mid-row) and scores
+# large enough that exponentials against a stale reference overflow.
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_growing_scores(D, causal, dtype):
+    q, k, v = make_inputs(1, 8, 2, 1024, 1024, D, torch.float32)
+    ramp = 0.1 + 4.0 * torch.arange(1024, dtype=torch.float32) / 1024
+    q, k, v = (t.to(dtype).to(DEV) for t in (q, k * ramp[None, None, :, None], v))
+    assert _route(q, k).kind == "single"
+    out = _run(q, k, v, causal)
+    assert_close(out, oracle(q, k, v, causal, dtype=np.float64), BASELINE_TOL[dtype], "growing scores")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_large_scores(D, dtype):
+    q, k, _ = make_inputs(1, 8, 2, 512, 512, D, torch.float32, scale=4.0)
+    _, _, v = make_inputs(1, 8, 2, 512, 512, D, torch.float32, seed=1)
+    q, k, v = (t.to(dtype).to(DEV) for t in (q, k, v))
+    out = _run(q, k, v)
+    assert_close(out, oracle(q, k, v, dtype=np.float64), BASELINE_TOL[dtype], "large scores")
+
+
 def test_empty_query():
     q, k, v = make_inputs(1, 8, 2, 0, 64, 128, device=DEV)
     out = _run(q, k, v)
