@@ -237,8 +237,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int sub = wave >> 1, mb = wave & 1;
   const char* mytile = smem + sub * ST::kBytes;
 
+  // Issue priority falls with progress (3 for the first quarter of the
+  // chunk, then 2, 1, 0).  Two workgroups share a compute unit; at equal
+  // priority the older one's waves issue first and it streams its chunk up
+  // to ~25 % ahead of its neighbour, which then finishes alone at a lower
+  // memory rate.  Ranking by progress keeps the two within a quarter of each
+  // other (the two end 5 instead of 19 µs apart at 131072 keys, ~2 % faster).
+  int prio_lvl = -1;
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = tile_key(it);
+    const int lvl = (4 * it) / ntiles;  // wave-uniform
+    if (lvl != prio_lvl) {
+      prio_lvl = lvl;
+      if (lvl == 0) __builtin_amdgcn_s_setprio(3);
+      else if (lvl == 1) __builtin_amdgcn_s_setprio(2);
+      else if (lvl == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     __syncthreads();  // previous tile fully consumed
     store_subtile<D>(smem, R0, t);
     store_subtile<D>(smem + ST::kBytes, R1, t);
@@ -288,6 +303,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     pv_block<DT, D>(mytile, pk, acc, mb, lane);
   }
 
+  __builtin_amdgcn_s_setprio(0);
   // Merge the 4 waves' states in LDS: m_s/l_s [wave][row], acc (reusing the
   // tile buffer, exactly 4 * D * 32 floats) as f32x4 at
   // [((wave * D/32 + db) * 4 + j) * 64 + lane].
