@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .gqa_split import _counter_buffer, _workspace_buffer, split_kv_forward
+from .gqa_split import _counter_buffer, _workspace_buffer, split_kv_forward, stream_handle
 
 __all__ = ["gqa_flash_attn", "Route", "choose_route"]
 
@@ -163,12 +163,17 @@ def _cu_count(device_index: int) -> int:
     return n
 
 
-def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+def _is_kernel_ready(t: torch.Tensor) -> bool:
     """The kernels need a unit last-dim stride and 16-byte aligned rows."""
-    es = t.element_size()
-    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0
-          and all((s * es) % 16 == 0 for s in t.stride()[:3]))
-    return t if ok else t.contiguous()
+    st = t.stride()
+    # 16-byte alignment of the pointer and of every stride in bytes, in one
+    # test (a multiple of 16 has its low four bits clear).
+    return st[3] == 1 and (t.data_ptr() | ((st[0] | st[1] | st[2]) * t.element_size())) % 16 == 0
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """t itself, or a fresh contiguous copy when the kernels cannot read it."""
+    return t if _is_kernel_ready(t) else t.clone(memory_format=torch.contiguous_format)
 
 
 def gqa_flash_attn(q, k, v, causal=True, *, return_lse=False):
@@ -215,7 +220,7 @@ def gqa_flash_attn(q, k, v, causal=True, *, return_lse=False):
             return split_kv_forward(q, k, v, causal, route.splits, return_lse=return_lse)
 
         o = torch.empty_like(q_in)  # as dispatch.py:47; contiguous if unusable
-        if _kernel_ready(o) is not o:
+        if not _is_kernel_ready(o):
             o = torch.empty_like(q_in, memory_format=torch.contiguous_format)
         return single_pass_forward(q, k, v, o, causal, route.fwd_split, return_lse)
 
@@ -229,7 +234,7 @@ def single_pass_forward(q, k, v, o, causal, fwd_split=0, return_lse=False):
     batch, num_heads, seq_q, head_dim = q.shape
     _, num_kv_heads, seq_kv, _ = k.shape
     scale_log2 = (head_dim ** -0.5) * LOG2E
-    stream = torch.cuda.current_stream(q.device).cuda_stream
+    stream = stream_handle(q.device)
     common = (batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
               scale_log2, int(bool(causal)), _DTYPES[q.dtype], stream)
     qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),

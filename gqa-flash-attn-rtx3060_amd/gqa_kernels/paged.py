@@ -39,7 +39,7 @@ from typing import Dict, Hashable, List, Optional, Sequence
 import torch
 
 from . import _lib
-from .gqa_split import _workspace_buffer, workspace_bytes
+from .gqa_split import _workspace_buffer, stream_handle, workspace_bytes
 
 __all__ = [
     "paged_attention",
@@ -215,7 +215,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
 
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
-    stream = torch.cuda.current_stream(q.device).cuda_stream
+    stream = stream_handle(q.device)
     route = route or paged_route(num_heads, num_kv_heads, seq_q, block_size)
     assert route in ("split", "single") and (route == "split" or block_size >= 64)
     lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if return_lse else None
@@ -265,7 +265,7 @@ def write_kv(key, value, k_cache, v_cache, slot_mapping):
     key = key if _rows_ready(key) else key.contiguous()
     value = value if _rows_ready(value) else value.contiguous()
     lib = _lib.load()
-    stream = torch.cuda.current_stream(key.device).cuda_stream
+    stream = stream_handle(key.device)
     _lib.check(lib.gqa_paged_cache_write_launch(
         key.data_ptr(), _lib.strides3(key), value.data_ptr(), _lib.strides3(value),
         k_cache.data_ptr(), _lib.strides(k_cache), v_cache.data_ptr(), _lib.strides(v_cache),

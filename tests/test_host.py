@@ -247,3 +247,25 @@ def test_package_exports():
     import gqa_kernels
     assert gqa_kernels.__all__ == ["gqa_flash_attn"]
     assert gqa_kernels.__version__ == "0.1.0"
+
+
+# ---------------------------------------------------------------------------
+# Layouts the kernels accept as they are, and copies of the others
+# ---------------------------------------------------------------------------
+def test_kernel_ready_layouts():
+    from gqa_kernels.dispatch import _is_kernel_ready, _kernel_ready
+    base = torch.zeros(2, 8, 64, 128, dtype=torch.bfloat16)
+    assert _is_kernel_ready(base) and _kernel_ready(base) is base
+    # (B, S, H, D) storage viewed as (B, H, S, D): strides of 16-byte rows
+    bshd = torch.zeros(2, 64, 8, 128, dtype=torch.bfloat16).transpose(1, 2)
+    assert _is_kernel_ready(bshd) and _kernel_ready(bshd) is bshd
+    cases = [
+        torch.zeros(2, 8, 128, 64, dtype=torch.bfloat16).transpose(2, 3),  # last-dim stride 64
+        torch.zeros(2 * 8 * 64 * 128 + 1, dtype=torch.bfloat16)[1:].view(2, 8, 64, 128),  # 2-byte offset
+        base.as_strided((2, 8, 1, 128), (8 * 64 * 128, 64 * 128, 3, 1)),  # odd stride on a size-1 dim
+        torch.zeros(2, 8, 64, 132, dtype=torch.bfloat16)[..., :128],  # 264-byte rows
+    ]
+    for t in cases:
+        assert not _is_kernel_ready(t)
+        c = _kernel_ready(t)
+        assert c is not t and _is_kernel_ready(c) and torch.equal(c, t)
