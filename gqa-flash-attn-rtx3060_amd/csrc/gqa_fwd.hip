@@ -562,8 +562,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   }
   if (grp == 0) phase_barrier();  // both groups pass the same number of barriers
   // No LDS-DMA load (of a tile past the end) may still be writing when the
-  // workgroup exits.
+  // stages are reused for the output below, nor when the workgroup exits.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
 
   // Split query block: publish this half's state (reference max, lane
   // partial row sum, accumulators, lane-major so each lane of the other
@@ -617,8 +618,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     const int64_t li = varlen ? (tok0 + pos) * dm.Hq + head : ((int64_t)b * dm.Hq + head) * dm.Sq + pos;
     p.lse[li] = (m_run * c + __log2f(l_tot)) * kLn2;
   }
-  if (valid) {
-    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(p.o, pos, head);
+  // The wave's 32 x D output tile goes through LDS (row-major, 16-byte
+  // chunks XOR-swizzled by row; two waves per former K/V stage), so that it
+  // leaves as whole rows: each store instruction writes 64 lanes x 16 bytes
+  // covering RPI complete rows, where storing straight from the O^T
+  // accumulators would write 16 bytes into each of 32 rows per instruction.
+  {
+    constexpr int CPR16 = 2 * D / 16;   // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR16;     // rows per store instruction
+    const int sw = wave >> 1;
+    char* ot = (sw == 0 ? sk0 : sw == 1 ? sk1 : sw == 2 ? sk2 : sv0) + (wave & 1) * (32 * 2 * D);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -626,8 +635,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
         u32x2 x;
         x[0] = E::pack2(acc[db][4 * j] * inv, acc[db][4 * j + 1] * inv);
         x[1] = E::pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * j + 4 * hh) = x;
+        const int ch = (4 * db + j) ^ (i & (CPR16 - 1));
+        *reinterpret_cast<u32x2*>(ot + i * (2 * D) + ch * 16 + 8 * hh) = x;
       }
+    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's LDS writes before its reads
+    const int c = lane % CPR16;
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int rr = RPI * it + lane / CPR16;  // row of the tile
+      const u32x4 x = *reinterpret_cast<const u32x4*>(ot + rr * (2 * D) + ((c ^ (rr & (CPR16 - 1))) * 16));
+      const int r2 = wave * 32 + rr;
+      const int g2 = r2 / p.block_m, pos2 = pid_m * p.block_m + (r2 - g2 * p.block_m);
+      if (g2 < dm.G && pos2 < sq) {
+        T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(p.o, pos2, kvh * dm.G + g2);
+        *reinterpret_cast<u32x4*>(orow + 8 * c) = x;
+      }
+    }
   }
 }
 
