@@ -292,17 +292,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   const int head = kvh * dm.G + (g < dm.G ? g : 0);
   const int qpos = pos + (skv - sq);
 
-  u32x4 qreg[NKS];
-  {
-    const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(p.q, valid ? pos : 0, head);
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      u32x4 x = {0u, 0u, 0u, 0u};
-      if (valid) x = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
-      qreg[ks] = x;
-    }
-  }
-
   // Key range of this workgroup.
   const int pos_lo = pid_m * p.block_m;
   const int pos_hi = min(pos_lo + p.block_m, sq) - 1;
@@ -405,13 +394,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   using BF = std::false_type;
 
   // Prologue: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1) of stage 2
-  // (tile indices relative to tb).
+  // (tile indices relative to tb).  The tile loads go first: the Q loads
+  // behind them touch 32 rows per instruction and, issued first, held the
+  // tile loads back by ~2 us.  An invalid row loads row 0 of its sequence
+  // (always present here) and is zeroed.
   if (grp == 0) {
     issue_k(sk0, tb);
     issue_k(sk1, tb + 1);
   } else {
     issue_v(sv1, tb);
     issue_v(sv2, tb + 1);
+  }
+  u32x4 qreg[NKS];
+  {
+    const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(p.q, valid ? pos : 0, head);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
+      qreg[ks] = valid ? x : u32x4{0u, 0u, 0u, 0u};
+    }
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // these loads and Q
   phase_barrier();
