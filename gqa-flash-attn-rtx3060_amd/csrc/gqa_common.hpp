@@ -145,6 +145,16 @@ __device__ inline u32x2 ld8(const void* p) {
   return *reinterpret_cast<const u32x2*>(p);
 }
 
+// Wave-uniform read of a value that no work-item writes during the launch
+// (block tables, per-sequence lengths) through the scalar cache.  Read as an
+// ordinary global load it would be a vector load whose s_waitcnt vmcnt(0)
+// also waits for every LDS-DMA tile load in flight.
+__device__ inline int load_uniform(const int* p) {
+  // Global and constant address-space pointers share one 64-bit address.
+  typedef const __attribute__((address_space(4))) int ConstInt;
+  return *(ConstInt*)(uintptr_t)p;
+}
+
 // Where the K or V row of key j of one (b, kv head) lives.
 //   Contiguous: base + j * row stride (the (B, H, S, D) tensors).
 //   Paged: a block table maps key j to slot j % block_size of block
@@ -161,6 +171,7 @@ struct ContigRows {
   const T* base;  // key 0 of this (b, kv head)
   int64_t ss;     // key stride (elements)
   __device__ const T* row(int key) const { return base + (int64_t)key * ss; }
+  __device__ const T* row_uniform(int key) const { return row(key); }
   __device__ static constexpr bool run64() { return true; }
 };
 template <typename T, bool kBigPages>
@@ -171,6 +182,10 @@ struct PagedRows {
   int shift;          // log2(block_size)
   __device__ const T* row(int key) const {
     return base + (int64_t)table[key >> shift] * sblk + (int64_t)(key & ((1 << shift) - 1)) * sss;
+  }
+  // The same for a key that is equal in every lane (scalar table read).
+  __device__ const T* row_uniform(int key) const {
+    return base + (int64_t)load_uniform(table + (key >> shift)) * sblk + (int64_t)(key & ((1 << shift) - 1)) * sss;
   }
   __device__ static constexpr bool run64() { return kBigPages; }
 };
@@ -186,8 +201,8 @@ __device__ inline void load_subtile(SubTileRegs<D>& R, const KR& kr, const KR& v
   constexpr int KPT = SubTileRegs<D>::KPT;
   if (key0 + 64 <= key_lim) {
     if constexpr (KR::run64()) {
-      const T* kb = kr.row(key0);
-      const T* vb = vr.row(key0);
+      const T* kb = kr.row_uniform(key0);
+      const T* vb = vr.row_uniform(key0);
 #pragma unroll
       for (int j = 0; j < SubTileRegs<D>::KCH; ++j) {
         const int ci = t + 256 * j;

@@ -274,10 +274,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   const int b = bh / dm.Hkv, kvh = bh - b * dm.Hkv;
   // Keys of this sequence (paged: its own length, clamped to [0, Skv]),
   // and its query rows (variable lengths: q_len[b], tokens from q_start[b]).
-  const int skv = PAGED ? min(max(p.seq_lens[b], 0), dm.Skv) : dm.Skv;
+  const int skv = PAGED ? min(max(load_uniform(p.seq_lens + b), 0), dm.Skv) : dm.Skv;
   const bool varlen = p.q_len != nullptr;
-  const int sq = varlen ? min(max(p.q_len[b], 0), dm.Sq) : dm.Sq;
-  const int64_t tok0 = varlen ? (int64_t)p.q_start[b] : 0;
+  const int sq = varlen ? min(max(load_uniform(p.q_len + b), 0), dm.Sq) : dm.Sq;
+  const int64_t tok0 = varlen ? (int64_t)load_uniform(p.q_start + b) : 0;
   if (pid_m * p.block_m >= sq) return;  // a block past this sequence's queries (variable lengths)
   // Element offset of (query row pos, head h) in q / o.
   auto row_off = [&](const TensorRef& t, int pos_, int h) -> int64_t {
@@ -330,25 +330,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // starts at the tile's first row and ends at the sequence's last key, so
   // rows past the sequence (and whole tiles past it, which read no table
   // entry) load as zeros.
+  // Paged: the block holding a tile (read only for tiles that start inside
+  // the sequence).  The softmax phases use a block id read one phase ahead
+  // (blk_next), so the table read's latency is off the issue path.
+  auto tile_block = [&](int tile) -> int {
+    const int key0 = tile * ST::kKeys;
+    return key0 < skv ? load_uniform(table_row + (key0 >> p.block_shift)) : 0;
+  };
   auto issue_tile = [&](char* lds, const char* head, __amdgpu_buffer_rsrc_t rsrc, uint32_t rowb, uint32_t off,
-                        int64_t blk_stride, int tile) {
+                        int64_t blk_stride, int tile, int blk) {
     if constexpr (PAGED) {
       const int key0 = tile * ST::kKeys;
       const int rows = skv - key0;
       __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
       if (rows > 0) {
-        const int blk = table_row[key0 >> p.block_shift];
         const char* base =
             head + 2 * ((int64_t)blk * blk_stride + (int64_t)(key0 & ((1 << p.block_shift) - 1)) * (rowb >> 1));
         rt = make_rsrc(base, (uint32_t)(min(rows, ST::kKeys) - 1) * rowb + 2 * D);
       }
       issue_tile_dma<D>(lds, rt, 0u, rowb, off, gw);
     } else {
+      (void)blk;
       issue_tile_dma<D>(lds, rsrc, (uint32_t)(tile * ST::kKeys) * rowb, rowb, off, gw);
     }
   };
-  auto issue_k = [&](char* lds, int tile) { issue_tile(lds, kbh, rk, kssb, koff, p.k.sb, tile); };
-  auto issue_v = [&](char* lds, int tile) { issue_tile(lds, vbh, rv, vssb, voff, p.v.sb, tile); };
+  auto issue_k = [&](char* lds, int tile, int blk) { issue_tile(lds, kbh, rk, kssb, koff, p.k.sb, tile, blk); };
+  auto issue_v = [&](char* lds, int tile, int blk) { issue_tile(lds, vbh, rv, vssb, voff, p.v.sb, tile, blk); };
 
   // LDS side: per-lane read offsets (the 32-key block, chunk and row offsets
   // of each read are immediates on top of these).  The masks are no-ops on
@@ -398,13 +405,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // behind them touch 32 rows per instruction and, issued first, held the
   // tile loads back by ~2 us.  An invalid row loads row 0 of its sequence
   // (always present here) and is zeroed.
+  int blk_next = 0;  // paged: block of the tile the next softmax phase issues
   if (grp == 0) {
-    issue_k(sk0, tb);
-    issue_k(sk1, tb + 1);
+    issue_k(sk0, tb, PAGED ? tile_block(tb) : 0);
+    issue_k(sk1, tb + 1, PAGED ? tile_block(tb + 1) : 0);
   } else {
-    issue_v(sv1, tb);
-    issue_v(sv2, tb + 1);
+    issue_v(sv1, tb, PAGED ? tile_block(tb) : 0);
+    issue_v(sv2, tb + 1, PAGED ? tile_block(tb + 1) : 0);
   }
+  if constexpr (PAGED) blk_next = tile_block(tb + 2);
   u32x4 qreg[NKS];
   {
     const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(p.q, valid ? pos : 0, head);
@@ -485,10 +494,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     __builtin_amdgcn_sched_barrier(0);
     const int ta = tb + tt;  // absolute tile index
     if (grp == 0) {
-      issue_k(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), ta + 2);
+      issue_k(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), ta + 2, blk_next);
     } else {
-      issue_v(vstage(s3), ta + 2);
+      issue_v(vstage(s3), ta + 2, blk_next);
     }
+    if constexpr (PAGED) blk_next = tile_block(ta + 3);
     const int key0 = ta * ST::kKeys;
     const bool need_mask = (key0 + ST::kKeys > skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
     if (need_mask) {

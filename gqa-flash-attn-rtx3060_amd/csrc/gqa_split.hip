@@ -159,12 +159,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // to [0, max_seq_len] so that no key past the block table's covered range
   // is ever addressed.
   constexpr bool PAGED = KV != 0;
-  const int skv = PAGED ? min(max(p.seq_lens[b], 0), dm.Skv) : dm.Skv;
+  const int skv = PAGED ? min(max(load_uniform(p.seq_lens + b), 0), dm.Skv) : dm.Skv;
   // Query rows of this sequence (variable lengths: q_len[b] rows, tokens
   // from q_start[b]; q token-major).
   const bool varlen = p.q_len != nullptr;
-  const int sq = varlen ? min(max(p.q_len[b], 0), dm.Sq) : dm.Sq;
-  const int64_t tok0 = varlen ? (int64_t)p.q_start[b] : 0;
+  const int sq = varlen ? min(max(load_uniform(p.q_len + b), 0), dm.Sq) : dm.Sq;
+  const int64_t tok0 = varlen ? (int64_t)load_uniform(p.q_start + b) : 0;
   if ((32 * rb) / dm.G >= sq) return;  // a row block past this sequence's queries
 
   // This lane's query row (position-major packing).
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   // partials; o and lse are token-major.
   const bool varlen = p.q_len != nullptr;
   if (varlen && pos >= p.q_len[b]) return;
-  const int64_t tok = varlen ? (int64_t)p.q_start[b] + pos : 0;
+  const int64_t tok = varlen ? (int64_t)load_uniform(p.q_start + b) + pos : 0;
   const float* wm = p.ws_m + (int64_t)row * S;
   const float* wl = p.ws_l + (int64_t)row * S;
   const float* wa = p.ws_acc + (int64_t)row * S * D;
