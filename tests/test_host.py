@@ -162,8 +162,11 @@ def test_route_baseline_configs():
     # decode 131072: split to 2 workgroups per CU
     r = choose_route(1, 32, 8, 1, 131072, cu)
     assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
-    # decode 8192: limited by the minimum chunk (256 keys)
+    # decode 8192: 2 workgroups per CU with 128-key chunks
     r = choose_route(1, 32, 8, 1, 8192, cu)
+    assert r.kind == "split" and r.splits == 64
+    # decode 4096: limited by the minimum chunk (one 128-key tile)
+    r = choose_route(1, 32, 8, 1, 4096, cu)
     assert r.kind == "split" and r.splits == 32
     # 70B multi-token decode: 32 packed rows per kv head, 128 (b, kv head) pairs
     r = choose_route(16, 64, 8, 4, 32768, cu)
