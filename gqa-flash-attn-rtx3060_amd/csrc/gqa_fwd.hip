@@ -581,29 +581,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // partial row sum, accumulators, lane-major so each lane of the other
   // item reads back exactly its own row); the item that completes the
   // block's counter merges the other half into its registers and writes o.
+  // The counter is read first: when the other half has already published
+  // (counter 1), this item is the last one and skips publishing its own.
+  // Otherwise it publishes, then counts itself in; whichever item's
+  // increment finds 1 merges.  Every increment follows its item's completed
+  // stores, so a counter of 1 means the other state is readable.
   if (part >= 0) {
     constexpr int PF_ = kFwdPartFloats(D);
     constexpr int NA = NDB * 16;  // accumulators per lane
     const int slot = bh * p.n_split + (p.n_mblk - 1 - pid_m);
     float* mine = p.part_ws + ((int64_t)slot * 2 + part) * PF_;
     const float* other = p.part_ws + ((int64_t)slot * 2 + (1 - part)) * PF_;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t, acc[db][v]);
-    store_coherent(mine + NA * kFwdThreads + t, m_run);
-    store_coherent(mine + (NA + 1) * kFwdThreads + t, l_run);
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
-    __syncthreads();
     __shared__ int s_last;
-    if (t == 0) {
-      const int prev = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (prev == 1);
-      // Both halves have arrived: leave the counter zero for the next call.
-      if (s_last) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (t == 0) s_last = __hip_atomic_load(&p.part_cnt[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
     __syncthreads();
-    if (!s_last) return;
+    if (!s_last) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t, acc[db][v]);
+      store_coherent(mine + NA * kFwdThreads + t, m_run);
+      store_coherent(mine + (NA + 1) * kFwdThreads + t, l_run);
+      __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+      __syncthreads();
+      if (t == 0) s_last = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+      __syncthreads();
+      if (!s_last) return;
+    }
+    // Both halves have arrived: leave the counter zero for the next call.
+    if (t == 0) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float m_o = load_coherent(other + NA * kFwdThreads + t);
     const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t);
     const float mm = fmaxf(m_run, m_o);
