@@ -610,17 +610,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     }
     // Both halves have arrived: leave the counter zero for the next call.
     if (t == 0) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The merge is written in terms of the lower (0) and upper (1) half, not
+    // of this item and the other one, so the rounding (fma contraction
+    // included) does not depend on which half finished last: repeated
+    // calls give identical outputs.
+    const bool lo = part == 0;
     const float m_o = load_coherent(other + NA * kFwdThreads + t);
     const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t);
-    const float mm = fmaxf(m_run, m_o);
+    const float m0 = lo ? m_run : m_o, m1 = lo ? m_o : m_run;
+    const float mm = fmaxf(m0, m1);
     const float mu = (mm == -__builtin_inff()) ? 0.f : mm;
-    const float a_s = fast_exp2((m_run - mu) * c), a_o = fast_exp2((m_o - mu) * c);
+    const float a0 = fast_exp2((m0 - mu) * c), a1 = fast_exp2((m1 - mu) * c);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int v = 0; v < 16; ++v)
-        acc[db][v] = acc[db][v] * a_s + load_coherent(other + (db * 16 + v) * kFwdThreads + t) * a_o;
-    l_run = l_run * a_s + l_o * a_o;
+      for (int v = 0; v < 16; ++v) {
+        const float x_o = load_coherent(other + (db * 16 + v) * kFwdThreads + t);
+        const float x0 = lo ? acc[db][v] : x_o, x1 = lo ? x_o : acc[db][v];
+        acc[db][v] = __builtin_fmaf(x0, a0, x1 * a1);
+      }
+    const float l0 = lo ? l_run : l_o, l1 = lo ? l_o : l_run;
+    l_run = __builtin_fmaf(l0, a0, l1 * a1);
     m_run = mm;
   }
 
