@@ -264,6 +264,8 @@ def test_split_count_invariance():
     (2, 8, 4, 1, 1100, 64),       # decode, head_dim 64, split path
     (1, 64, 8, 4, 3000, 128),     # 70B group, split path
     (1, 8, 2, 1, 77, 128),        # short decode, single-pass path
+    (1, 32, 2, 70, 300, 128),     # G = 16: a wave's 32 output rows span two heads
+    (2, 16, 8, 300, 300, 64),     # G = 2, head_dim 64, ragged last block
 ])
 @pytest.mark.parametrize("causal", [True, False])
 def test_shapes(B, Hq, Hkv, Sq, Skv, D, causal):
