@@ -96,6 +96,15 @@ def test_baseline_prefill_large(seq):
     assert mx <= 2e-2 and mn <= 2e-3, (mx, mn)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_head_dim64_large(dtype):
+    # head_dim 64 runs at four waves per SIMD (two workgroups per CU).
+    q, k, v = make_inputs(1, 32, 8, 8192, 8192, 64, dtype, device=DEV)
+    out = _run(q, k, v)
+    rows = np.r_[0:64, 4096 - 32:4096 + 32, 8192 - 64:8192]
+    assert_close(out[:, :, rows], oracle(q, k, v, rows=rows), BASELINE_TOL[dtype], "D=64 8192")
+
+
 @pytest.mark.parametrize("seq_kv", [8192, 32768, 131072])
 def test_baseline_decode(seq_kv):
     q, k, v = make_inputs(1, 32, 8, 1, seq_kv, 128, device=DEV)
