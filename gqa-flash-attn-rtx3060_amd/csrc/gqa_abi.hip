@@ -67,7 +67,9 @@ const char* gqa_strerror(int code) {
     case GQA_E_STRIDE:
       return "unsupported layout: last dim must be contiguous, rows 16-byte aligned, and one head's K/V rows "
              "within 2 GiB";
-    case GQA_E_SPLITS: return "splits out of range [1, GQA_MAX_SPLITS]";
+    case GQA_E_SPLITS:
+      return "splits out of range [1, GQA_MAX_SPLITS], or a paged chunk spans more than "
+             "GQA_PAGED_CHUNK_PAGES pages of under 64 keys";
     case GQA_E_GROUP: return "group size (num_heads / num_kv_heads) larger than 256";
     case GQA_E_NULL: return "null pointer argument";
     case GQA_E_BLOCK:
@@ -269,6 +271,9 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4], const
   int shift = 0;
   while ((1 << shift) < block_size) ++shift;
   p.block_shift = shift;
+  // Pages under 64 keys: each workgroup stages its chunk's table slice in LDS.
+  static_assert(gqa::kPagedTableMax == GQA_PAGED_CHUNK_PAGES, "table slice size");
+  if (shift < 6 && (p.chunk >> shift) > gqa::kPagedTableMax) return GQA_E_SPLITS;
   p.rotate = p.k.ss == head_dim && p.v.ss == head_dim;
   p.q_start = q_start;
   p.q_len = q_len;

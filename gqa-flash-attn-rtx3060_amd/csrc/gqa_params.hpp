@@ -111,6 +111,9 @@ constexpr int kSplitTileKeys = 128;
 // The fused combine stages (valid rows of a 32-row block) x splits values in
 // LDS; above this the separate combine kernel is used.
 constexpr int kFusedMaxRowSplitsHost = 4096;
+// Block-table entries a split-KV workgroup over pages of fewer than 64 keys
+// copies to LDS (8 KiB): its chunk may span at most this many pages.
+constexpr int kPagedTableMax = 2048;
 
 // Paged cache write: new tokens (num_tokens, Hkv, D) into
 // (num_blocks, block_size, Hkv, D) caches at slot_mapping[t].

@@ -25,7 +25,7 @@
 // through the block table (PagedRows).  With pages of >= 64 keys (KV = 1) a
 // 64-key sub-tile is one strided run inside one page and loads like a
 // contiguous tile after one table lookup; smaller pages (KV = 2) resolve the
-// page of every row.
+// page of every row, from a copy of the chunk's table slice in LDS.
 #include <type_traits>
 
 #include "gqa_common.hpp"
@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int kSmemBytes = 2 * ST::kBytes > kCombineBytes ? 2 * ST::kBytes : kCombineBytes;
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
   __shared__ float m_s[128], l_s[128];
+  __shared__ int s_tab[KV == 2 ? kPagedTableMax : 1];
 
   const Dims& dm = p.dm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -201,6 +202,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   Rows kr, vr;
   if constexpr (PAGED) {
     const int* table = p.block_table + (int64_t)b * p.table_stride;
+    if constexpr (KV == 2) {
+      // Pages under 64 keys: every key row resolves its own page, so the
+      // chunk's slice of the block table is copied to LDS once and the
+      // per-row lookups read it there (LDS reads) instead of re-reading
+      // global memory on the load path.  The launch rejects chunks of more
+      // than kPagedTableMax pages; the bound on the copy keeps LDS safe
+      // regardless.
+      const int p0 = c0 >> p.block_shift;
+      const int np = c1 > c0 ? ((c1 - 1) >> p.block_shift) - p0 + 1 : 0;
+      for (int e = t; e < np && e < kPagedTableMax; e += 256) s_tab[e] = table[p0 + e];
+      __syncthreads();
+      table = s_tab - p0;
+    }
     kr = Rows{static_cast<const T*>(p.k.ptr) + (int64_t)kvh * p.k.sh, table, p.k.sb, p.k.ss, p.block_shift};
     vr = Rows{static_cast<const T*>(p.v.ptr) + (int64_t)kvh * p.v.sh, table, p.v.sb, p.v.ss, p.block_shift};
   } else {

@@ -44,6 +44,7 @@ from .gqa_split import _workspace_buffer, stream_handle, workspace_bytes
 __all__ = [
     "paged_attention",
     "write_kv",
+    "paged_chunk",
     "paged_splits",
     "PagedKVCache",
     "PagedAttentionMetadata",
@@ -75,11 +76,20 @@ def _cu_count(device_index: int) -> int:
         return n
 
 
+def paged_chunk(max_seq_len: int, splits: int) -> int:
+    """Keys per split chunk of the paged first pass: ceil(max_seq_len /
+    splits) rounded up to a multiple of 64 (as gqa_paged_split_first_launch
+    computes it)."""
+    return (-(-max_seq_len // splits) + 63) & ~63
+
+
 def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
-                 cu_count: int) -> int:
+                 cu_count: int, block_size: int = 64) -> int:
     """Split count for a paged call: the power of two that brings the first
     pass to two workgroups per compute unit while every chunk keeps at least
-    256 keys (pure function of the shapes)."""
+    256 keys (pure function of the shapes).  With pages under 64 keys a chunk
+    spans at most GQA_PAGED_CHUNK_PAGES pages (the slice of the block table a
+    workgroup stages in LDS), which can ask for more splits."""
     group = num_heads // num_kv_heads
     base = -(-group * seq_q // _SPLIT_ROWS) * num_kv_heads * batch
     target = _SPLIT_WG_PER_CU * cu_count
@@ -87,6 +97,10 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
     while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
            and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
         splits *= 2
+    if block_size < 64:
+        while (paged_chunk(max_seq_len, splits) // block_size > _lib.GQA_PAGED_CHUNK_PAGES
+               and splits < _lib.GQA_MAX_SPLITS):
+            splits *= 2
     return splits
 
 
@@ -197,7 +211,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     assert 0 <= max_seq_len <= capacity, "max_seq_len exceeds the block table's capacity"
     dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
     if splits is None:
-        splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev))
+        splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), block_size)
     if scale is None:
         scale = head_dim ** -0.5
 

@@ -43,7 +43,8 @@ extern "C" {
 #define GQA_E_DTYPE (-3)      /* dtype code not GQA_DTYPE_BF16 / GQA_DTYPE_FP16 */
 #define GQA_E_STRIDE (-4)     /* last-dim stride != 1, rows not 16-byte aligned, or (single
                                  pass) (seq_kv + 192) * row stride * 2 bytes >= 2^31 */
-#define GQA_E_SPLITS (-5)     /* splits outside [1, GQA_MAX_SPLITS] */
+#define GQA_E_SPLITS (-5)     /* splits outside [1, GQA_MAX_SPLITS], or chunk over
+                                 GQA_PAGED_CHUNK_PAGES small pages */
 #define GQA_E_GROUP (-6)      /* group size above what one packed tile holds */
 #define GQA_E_NULL (-7)       /* null pointer argument */
 #define GQA_E_BLOCK (-8)      /* paged cache: block_size not a power of two in
@@ -51,6 +52,7 @@ extern "C" {
 
 #define GQA_MAX_SPLITS 1024
 #define GQA_MAX_BLOCK_SIZE 65536
+#define GQA_PAGED_CHUNK_PAGES 2048 /* pages per split chunk when block_size < 64 */
 
 /* ABI revision; bumped when a signature below changes. */
 int gqa_abi_version(void);
@@ -217,7 +219,9 @@ int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4],
  * [0, max_seq_len]; keys past it are not read) and sets the chunk size: chunk s covers keys
  * [s*C, (s+1)*C) with C = ceil(max_seq_len / splits) rounded up to a
  * multiple of 64.  Every table entry a sequence reaches must index a block
- * of the caches; table_stride * block_size >= max_seq_len. */
+ * of the caches; table_stride * block_size >= max_seq_len.  With
+ * block_size < 64 a chunk may span at most GQA_PAGED_CHUNK_PAGES pages
+ * (C / block_size <= 2048), else GQA_E_SPLITS: raise splits. */
 int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4],
                                  const void* k_cache, const int64_t k_cache_stride[4],
                                  const void* v_cache, const int64_t v_cache_stride[4],

@@ -163,6 +163,32 @@ def test_paged_split_counts(splits):
     _check(o, None, q, kc, vc, table, seq_lens, True, torch.bfloat16)
 
 
+@pytest.mark.parametrize("bs,max_len,splits", [(1, 4096, 2), (1, 4096, None), (16, 40000, 2), (4, 8000, 1)])
+def test_paged_small_pages_table_slice(bs, max_len, splits):
+    """Pages under 64 keys: each workgroup stages its chunk's block-table
+    slice in LDS; (1, 4096, 2) and (16, 40000, 2) put 2048 and 1252 pages
+    in a chunk (2048 is the most a chunk may span), None is the host's own
+    split choice."""
+    from gqa_kernels.paged import paged_attention
+    q, kc, vc, table, seq_lens = _paged_inputs(2, 32, 8, 1, [max_len, max_len // 2 + 3], 128, bs,
+                                               torch.bfloat16, seed=11)
+    o, lse = paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), True,
+                             max_seq_len=max_len, splits=splits, return_lse=True)
+    torch.cuda.synchronize()
+    _check(o, lse, q, kc, vc, table, seq_lens, True, torch.bfloat16)
+
+
+@pytest.mark.parametrize("bs,max_len", [(1, 4096), (16, 40000)])
+def test_paged_small_pages_rejects_oversized_chunks(bs, max_len):
+    """One split over more than 2048 pages is refused before any launch."""
+    from gqa_kernels import _lib
+    from gqa_kernels.paged import paged_attention
+    q, kc, vc, table, seq_lens = _paged_inputs(1, 32, 8, 1, [max_len], 128, bs, torch.bfloat16, seed=12)
+    with pytest.raises(_lib.GQAError, match="-5"):
+        paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), True,
+                        max_seq_len=max_len, splits=1)
+
+
 def test_paged_equals_contiguous_at_decode_scale():
     """131072 keys in 128-key pages (shuffled) vs the contiguous split-KV
     route on the same K/V: same math, different chunking."""

@@ -112,6 +112,10 @@ def _paged(lib, **kw):
     (dict(D=96), -2), (dict(dtype=5), -3), (dict(Hq=30), -1), (dict(max_len=-1), -1),
     (dict(qstart=_FAKE), -7), (dict(qlen=_FAKE), -7),                # variable lengths need both
     (dict(qstart=_FAKE, qlen=ctypes.c_void_p((1 << 20) + 2)), -4),
+    # pages under 64 keys: one chunk spans at most 2048 of them
+    (dict(bs=1, tstride=4096, max_len=4096, splits=1), -5),
+    (dict(bs=16, tstride=4096, max_len=65536, splits=1), -5),
+    (dict(bs=32, tstride=4096, max_len=131072, splits=1), -5),
 ])
 def test_paged_first_validation(lib, kw, code):
     assert _paged(lib, **kw) == code
@@ -216,6 +220,24 @@ def test_paged_splits():
             s = paged_splits(B, 32, 8, 1, L, 256)
             assert s & (s - 1) == 0
             assert s == 1 or -(-L // s) >= 256
+
+
+def test_paged_splits_small_pages():
+    from gqa_kernels import _lib
+    from gqa_kernels.paged import paged_chunk, paged_splits
+    assert paged_chunk(4096, 2) == 2048 and paged_chunk(300, 1) == 320 and paged_chunk(40000, 2) == 20032
+    # 512 workgroups from the batch alone: one split, unless a chunk would
+    # span more than 2048 pages
+    assert paged_splits(512, 8, 1, 1, 4096, 256) == 1
+    assert paged_splits(512, 8, 1, 1, 4096, 256, block_size=64) == 1
+    assert paged_splits(512, 8, 1, 1, 4096, 256, block_size=1) == 2
+    assert paged_splits(512, 8, 1, 1, 1 << 20, 256, block_size=16) == 32
+    for bs in (1, 2, 4, 8, 16, 32):
+        for L in (1, 300, 2048, 2049, 70000, 1 << 20):
+            for B in (1, 64, 512):
+                s = paged_splits(B, 32, 8, 1, L, 256, block_size=bs)
+                assert s & (s - 1) == 0 and s <= _lib.GQA_MAX_SPLITS
+                assert paged_chunk(L, s) // bs <= _lib.GQA_PAGED_CHUNK_PAGES
 
 
 # ---------------------------------------------------------------------------
