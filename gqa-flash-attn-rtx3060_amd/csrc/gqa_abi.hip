@@ -291,7 +291,9 @@ int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4], const void* k
   if (rc) return rc;
   const int G = num_heads / num_kv_heads;
   if (G > gqa::kFwdRows) return GQA_E_GROUP;
-  if (block_size < 64 || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
+  // Each LDS-DMA instruction loads 512 / head_dim rows, which must lie in
+  // one block.
+  if (block_size < 512 / head_dim || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
     return GQA_E_BLOCK;
   if (table_stride < 0 || (int64_t)table_stride * block_size < (int64_t)max_seq_len) return GQA_E_BLOCK;
   if (batch == 0 || seq_q == 0) return GQA_OK;

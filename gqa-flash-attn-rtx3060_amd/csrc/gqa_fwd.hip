@@ -221,17 +221,25 @@ __device__ __forceinline__ void mphase_pipe() {
   }
 }
 
-// PAGED: K/V tiles come from a paged cache through the block table (one
-// buffer descriptor per 64-key tile, ending at the sequence's last key).
+// PG: 0 contiguous K/V; 1 a paged cache through the block table with pages
+// of >= 64 keys (one buffer descriptor per 64-key tile, ending at the
+// sequence's last key); 2 pages of RPI..32 keys (RPI = 512 / D rows per
+// LDS-DMA instruction: each instruction's rows lie in one page, and every
+// instruction gets its own descriptor).
 // D = 64 keeps to 128 VGPRs (four waves per SIMD): two workgroups share a
 // compute unit, which outweighs the shorter LDS-read lookahead it needs.
-template <int DT, int D, bool PAGED>
+template <int DT, int D, int PG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void gqa_fwd_kernel(
     FwdParams p) {
   using E = Elem<DT>;
   using T = typename E::T;
   using ST = FwdStage<D>;
   constexpr int CPR = ST::CPR;
+  constexpr bool PAGED = PG != 0;
+  constexpr bool SMALL = PG == 2;
+  // Block ids a wave needs per tile: one, or (small pages) one per LDS-DMA
+  // instruction it issues.
+  struct TileBlocks { int id[SMALL ? ST::NI : 1]; };
   constexpr int NDB = D / 32;  // 32-wide d blocks of O^T
   constexpr int NKS = D / 16;  // k-steps of S^T
   constexpr int PF = (D == 64) ? 4 : 6;  // MFMA slots of LDS-read lookahead
@@ -333,29 +341,61 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // Paged: the block holding a tile (read only for tiles that start inside
   // the sequence).  The softmax phases use a block id read one phase ahead
   // (blk_next), so the table read's latency is off the issue path.
-  auto tile_block = [&](int tile) -> int {
+  auto tile_block = [&](int tile) -> TileBlocks {
+    TileBlocks tbk;
     const int key0 = tile * ST::kKeys;
-    return key0 < skv ? load_uniform(table_row + (key0 >> p.block_shift)) : 0;
+    if constexpr (SMALL) {
+#pragma unroll
+      for (int j = 0; j < ST::NI; ++j) {
+        const int key = key0 + (j * 4 + gw) * ST::RPI;  // first row of instruction j
+        tbk.id[j] = key < skv ? load_uniform(table_row + (key >> p.block_shift)) : 0;
+      }
+    } else {
+      tbk.id[0] = (PAGED && key0 < skv) ? load_uniform(table_row + (key0 >> p.block_shift)) : 0;
+    }
+    return tbk;
   };
   auto issue_tile = [&](char* lds, const char* head, __amdgpu_buffer_rsrc_t rsrc, uint32_t rowb, uint32_t off,
-                        int64_t blk_stride, int tile, int blk) {
-    if constexpr (PAGED) {
-      const int key0 = tile * ST::kKeys;
+                        int64_t blk_stride, int tile, const TileBlocks& blk) {
+    const int key0 = tile * ST::kKeys;
+    if constexpr (SMALL) {
+      // Instruction j loads rows [key, key + RPI) of the tile, one run in
+      // one page (key is a multiple of RPI and pages hold >= RPI keys); its
+      // descriptor ends at the sequence's last key.
+      typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+      for (int j = 0; j < ST::NI; ++j) {
+        const int step = j * 4 + gw;
+        const int key = key0 + step * ST::RPI;
+        const int rows = skv - key;
+        __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
+        if (rows > 0) {
+          const char* base = head + 2 * ((int64_t)blk.id[j] * blk_stride +
+                                         (int64_t)(key & ((1 << p.block_shift) - 1)) * (rowb >> 1));
+          rt = make_rsrc(base, (uint32_t)(min(rows, ST::RPI) - 1) * rowb + 2 * D);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(lds + step * 1024), 16, off, 0, 0, 0);
+      }
+    } else if constexpr (PAGED) {
       const int rows = skv - key0;
       __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
       if (rows > 0) {
         const char* base =
-            head + 2 * ((int64_t)blk * blk_stride + (int64_t)(key0 & ((1 << p.block_shift) - 1)) * (rowb >> 1));
+            head + 2 * ((int64_t)blk.id[0] * blk_stride + (int64_t)(key0 & ((1 << p.block_shift) - 1)) * (rowb >> 1));
         rt = make_rsrc(base, (uint32_t)(min(rows, ST::kKeys) - 1) * rowb + 2 * D);
       }
       issue_tile_dma<D>(lds, rt, 0u, rowb, off, gw);
     } else {
       (void)blk;
-      issue_tile_dma<D>(lds, rsrc, (uint32_t)(tile * ST::kKeys) * rowb, rowb, off, gw);
+      issue_tile_dma<D>(lds, rsrc, (uint32_t)key0 * rowb, rowb, off, gw);
     }
   };
-  auto issue_k = [&](char* lds, int tile, int blk) { issue_tile(lds, kbh, rk, kssb, koff, p.k.sb, tile, blk); };
-  auto issue_v = [&](char* lds, int tile, int blk) { issue_tile(lds, vbh, rv, vssb, voff, p.v.sb, tile, blk); };
+  auto issue_k = [&](char* lds, int tile, const TileBlocks& blk) {
+    issue_tile(lds, kbh, rk, kssb, koff, p.k.sb, tile, blk);
+  };
+  auto issue_v = [&](char* lds, int tile, const TileBlocks& blk) {
+    issue_tile(lds, vbh, rv, vssb, voff, p.v.sb, tile, blk);
+  };
 
   // LDS side: per-lane read offsets (the 32-key block, chunk and row offsets
   // of each read are immediates on top of these).  The masks are no-ops on
@@ -405,15 +445,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // behind them touch 32 rows per instruction and, issued first, held the
   // tile loads back by ~2 us.  An invalid row loads row 0 of its sequence
   // (always present here) and is zeroed.
-  int blk_next = 0;  // paged: block of the tile the next softmax phase issues
+  // Paged: the block(s) of the tile the next softmax phase issues.
+  TileBlocks blk_next = tile_block(tb);
   if (grp == 0) {
-    issue_k(sk0, tb, PAGED ? tile_block(tb) : 0);
-    issue_k(sk1, tb + 1, PAGED ? tile_block(tb + 1) : 0);
+    issue_k(sk0, tb, blk_next);
   } else {
-    issue_v(sv1, tb, PAGED ? tile_block(tb) : 0);
-    issue_v(sv2, tb + 1, PAGED ? tile_block(tb + 1) : 0);
+    issue_v(sv1, tb, blk_next);
   }
-  if constexpr (PAGED) blk_next = tile_block(tb + 2);
+  blk_next = tile_block(tb + 1);
+  if (grp == 0) {
+    issue_k(sk1, tb + 1, blk_next);
+  } else {
+    issue_v(sv2, tb + 1, blk_next);
+  }
+  blk_next = tile_block(tb + 2);
   u32x4 qreg[NKS];
   {
     const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(p.q, valid ? pos : 0, head);
@@ -498,7 +543,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     } else {
       issue_v(vstage(s3), ta + 2, blk_next);
     }
-    if constexpr (PAGED) blk_next = tile_block(ta + 3);
+    blk_next = tile_block(ta + 3);
     const int key0 = ta * ST::kKeys;
     const bool need_mask = (key0 + ST::kKeys > skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
     if (need_mask) {
@@ -681,25 +726,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   }
 }
 
-template <int DT, int D, bool PAGED>
+template <int DT, int D, int PG>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   const int total = (p.n_mblk + p.n_split) * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PAGED>), dim3(total), dim3(kFwdThreads), 0, stream, p);
+  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(total), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();
 }
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
   if (dtype == 0)
-    return p.dm.D == 128 ? launch_fwd_t<0, 128, false>(p, stream) : launch_fwd_t<0, 64, false>(p, stream);
-  return p.dm.D == 128 ? launch_fwd_t<1, 128, false>(p, stream) : launch_fwd_t<1, 64, false>(p, stream);
+    return p.dm.D == 128 ? launch_fwd_t<0, 128, 0>(p, stream) : launch_fwd_t<0, 64, 0>(p, stream);
+  return p.dm.D == 128 ? launch_fwd_t<1, 128, 0>(p, stream) : launch_fwd_t<1, 64, 0>(p, stream);
 }
 
-// Requires block_size >= 64 (a 64-key tile lies in one block).
-hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
+template <int PG>
+static hipError_t launch_paged_fwd_t(const FwdParams& p, int dtype, hipStream_t stream) {
   if (dtype == 0)
-    return p.dm.D == 128 ? launch_fwd_t<0, 128, true>(p, stream) : launch_fwd_t<0, 64, true>(p, stream);
-  return p.dm.D == 128 ? launch_fwd_t<1, 128, true>(p, stream) : launch_fwd_t<1, 64, true>(p, stream);
+    return p.dm.D == 128 ? launch_fwd_t<0, 128, PG>(p, stream) : launch_fwd_t<0, 64, PG>(p, stream);
+  return p.dm.D == 128 ? launch_fwd_t<1, 128, PG>(p, stream) : launch_fwd_t<1, 64, PG>(p, stream);
+}
+
+// Requires block_size >= 512 / D, the rows of one LDS-DMA instruction
+// (pages of >= 64 keys hold whole tiles; smaller ones whole instructions).
+hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
+  if ((1 << p.block_shift) < 512 / p.dm.D) return hipErrorInvalidValue;
+  return p.block_shift >= 6 ? launch_paged_fwd_t<1>(p, dtype, stream) : launch_paged_fwd_t<2>(p, dtype, stream);
 }
 
 }  // namespace gqa

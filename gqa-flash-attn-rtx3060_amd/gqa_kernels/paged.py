@@ -12,8 +12,8 @@ of the above is in this repo").  This module is that step on MI355X:
   speculative verification) the split-KV pass (libgqa_hip.so
   ``gqa_paged_split_first_launch`` + ``gqa_split_reduce[_lse]_launch``), for
   longer ones (chunked prefill against a cached prefix) the single-pass
-  kernel loading each 64-key tile from its block
-  (``gqa_paged_fwd_launch``, blocks of >= 64 keys).
+  kernel loading each tile from its block(s)
+  (``gqa_paged_fwd_launch``, blocks of >= 512 / head_dim keys).
 * ``write_kv`` — store new tokens' K/V at their cache slots
   (``gqa_paged_cache_write_launch``).
 * ``PagedKVCache`` — host-side block allocator with reference-counted blocks:
@@ -121,11 +121,19 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> int:
     return block_size
 
 
-def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int) -> str:
+def single_pass_min_block(head_dim: int) -> int:
+    """Smallest block_size the single-pass paged kernel takes: the 512 /
+    head_dim rows one of its LDS-DMA instructions loads must lie in one
+    block."""
+    return 512 // head_dim
+
+
+def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int, head_dim: int = 128) -> str:
     """"split" (split-KV first pass + combine) for short query blocks, as the
     contiguous decode route; "single" (the single-pass kernel loading each
-    64-key tile from its block) for longer ones when blocks hold >= 64 keys."""
-    if (num_heads // num_kv_heads) * seq_q <= _SPLIT_MAX_ROWS or block_size < 64:
+    tile from its blocks) for longer ones when blocks hold at least
+    single_pass_min_block(head_dim) keys."""
+    if (num_heads // num_kv_heads) * seq_q <= _SPLIT_MAX_ROWS or block_size < single_pass_min_block(head_dim):
         return "split"
     return "single"
 
@@ -161,7 +169,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
         out: optional (batch, num_heads, seq_q, head_dim) tensor of q's dtype
             (any strides with 16-byte aligned rows) to write o into.
         route: "split" or "single" to force a kernel (default: paged_route;
-            "single" needs block_size >= 64).
+            "single" needs block_size >= 512 / head_dim).
         query_start, query_lens, max_query_len: variable query lengths.  q
             is then token-major (num_tokens, num_heads, head_dim); sequence
             b's queries are tokens query_start[b] .. + query_lens[b] - 1
@@ -230,8 +238,8 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
     stream = stream_handle(q.device)
-    route = route or paged_route(num_heads, num_kv_heads, seq_q, block_size)
-    assert route in ("split", "single") and (route == "split" or block_size >= 64)
+    route = route or paged_route(num_heads, num_kv_heads, seq_q, block_size, head_dim)
+    assert route in ("split", "single") and (route == "split" or block_size >= single_pass_min_block(head_dim))
     lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if return_lse else None
     lse_p = None if lse is None else lse.data_ptr()
     if route == "single":
@@ -523,7 +531,7 @@ class GQAPagedAttention(torch.nn.Module):
         groups: Dict[str, List[int]] = {}
         for b, ql in enumerate(md.query_lens):
             if ql > 0:
-                groups.setdefault(paged_route(H, Hkv, ql, k_cache.shape[1]), []).append(b)
+                groups.setdefault(paged_route(H, Hkv, ql, k_cache.shape[1], k_cache.shape[3]), []).append(b)
         dev = query.device
         for route, idx in groups.items():
             sel = torch.tensor(idx, dtype=torch.int64).to(dev)

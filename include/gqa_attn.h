@@ -236,8 +236,9 @@ int gqa_paged_split_first_launch(const void* q, const int64_t q_stride[4],
 
 /* Single-pass forward over a paged cache, for query blocks too large for the
  * split-KV pass (chunked prefill against a cached prefix): the kernel of
- * gqa_fwd_launch with each 64-key K/V tile loaded from its block, so
- * block_size must be a power of two >= 64.  Caches, block_table, seq_lens,
+ * gqa_fwd_launch with each K/V tile loaded from its blocks, so block_size
+ * must be a power of two >= 512 / head_dim (4 for head_dim 128, 8 for 64:
+ * the rows of one LDS-DMA instruction).  Caches, block_table, seq_lens,
  * max_seq_len and the causal alignment as gqa_paged_split_first_launch;
  * q and o are (batch, num_heads, seq_q, head_dim); lse may be NULL (no side
  * output) or as in gqa_fwd_lse_launch. */

@@ -94,12 +94,20 @@ def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, caus
     (3, 64, 8, 40, [1000, 41, 2500], 128, 256, torch.bfloat16, True, False),  # G = 8, sequence == chunk
     (2, 32, 8, 200, [150, 1000], 128, 64, torch.bfloat16, True, True),       # shorter than the chunk: masked rows
     (2, 16, 4, 70, [700, 333], 64, 64, torch.float16, False, False),         # D = 64, fp16, non-causal
+    # pages under 64 keys: one descriptor per LDS-DMA instruction (4 rows at
+    # D = 128, 8 at D = 64); ragged lengths end inside an instruction's rows
+    (2, 32, 8, 100, [3001, 150], 128, 16, torch.bfloat16, True, False),      # vLLM's 16-key blocks, NHD
+    (1, 32, 8, 300, [2047], 128, 16, torch.bfloat16, True, True),            # 16-key blocks, HND
+    (2, 32, 8, 90, [1030, 91], 128, 4, torch.bfloat16, True, False),         # smallest block at D = 128
+    (2, 32, 8, 90, [999, 400], 128, 32, torch.float16, False, True),         # 32-key blocks, fp16
+    (2, 16, 4, 70, [701, 333], 64, 8, torch.float16, True, False),           # smallest block at D = 64
+    (1, 16, 2, 120, [1500], 64, 16, torch.bfloat16, False, True),            # D = 64, 16-key HND
 ])
 def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal, hnd):
     """Query blocks above the split-KV size take the single-pass kernel with
-    each 64-key tile loaded from its block."""
+    each tile loaded from its block(s)."""
     from gqa_kernels.paged import paged_attention, paged_route
-    assert paged_route(Hq, Hkv, Sq, bs) == "single"
+    assert paged_route(Hq, Hkv, Sq, bs, D) == "single"
     q, kc, vc, table, seq_lens = _paged_inputs(B, Hq, Hkv, Sq, lens, D, bs, dtype, seed=sum(lens) + 1, hnd=hnd)
     print(f"paged single B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} lens={lens} D={D} bs={bs} {dtype} hnd={hnd}", flush=True)
     kd, vd = kc.to(DEV), vc.to(DEV)

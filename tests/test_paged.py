@@ -165,7 +165,8 @@ def _pfwd(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(bs=32), -8), (dict(bs=96), -8), (dict(bs=1 << 17), -8),   # blocks of >= 64 keys, power of two
+    (dict(bs=2), -8), (dict(bs=96), -8), (dict(bs=1 << 17), -8),    # blocks of >= 512 / D keys, power of two
+    (dict(bs=4, D=64, tstride=256), -8),                            # D = 64: 8 rows per instruction
     (dict(tstride=15), -8),
     (dict(lens=None), -7), (dict(table=None), -7), (dict(o=None), -7),
     (dict(lens=ctypes.c_void_p((1 << 20) + 2)), -4),
@@ -198,7 +199,11 @@ def test_paged_route():
     assert paged_route(32, 8, 1, 16) == "split"      # decode
     assert paged_route(32, 8, 16, 64) == "split"     # 64 packed rows
     assert paged_route(32, 8, 17, 64) == "single"
-    assert paged_route(32, 8, 512, 16) == "split"    # blocks below one 64-key tile
+    assert paged_route(32, 8, 512, 16) == "single"   # 16-key blocks: one descriptor per 4-row instruction
+    assert paged_route(32, 8, 512, 4) == "single"
+    assert paged_route(32, 8, 512, 2) == "split"     # below one instruction's rows at D = 128
+    assert paged_route(32, 8, 512, 4, 64) == "split"  # D = 64: 8 rows per instruction
+    assert paged_route(32, 8, 512, 8, 64) == "single"
     assert paged_route(64, 8, 9, 128) == "single"
 
 
