@@ -394,7 +394,8 @@ def paged_decode(torch, steps, warmup, traffic=None):
 def paged_prefill(torch, steps, warmup):
     """The chunked-prefill BASELINE shape (B=4, 512 new tokens attending 8192
     keys, causal) over a paged cache (gqa_kernels.paged, single-pass route),
-    128-key HND blocks and 64-key NHD blocks in random order."""
+    128-key HND blocks, 64-key NHD blocks and 16-key NHD blocks (vLLM's
+    default block size) in random order."""
     from gqa_kernels.paged import paged_attention
     b, sq, skv = 4, 512, 8192
     g = torch.Generator(device="cuda").manual_seed(4)
@@ -402,7 +403,7 @@ def paged_prefill(torch, steps, warmup):
     lens = torch.full((b,), skv, dtype=torch.int32, device="cuda")
     fl = flops(b, HQ, sq, skv, D)
     out = []
-    for bs, layout in ((128, "HND"), (64, "NHD")):
+    for bs, layout in ((128, "HND"), (64, "NHD"), (16, "NHD")):
         nblk = b * skv // bs
         shape = (nblk, HKV, bs, D) if layout == "HND" else (nblk, bs, HKV, D)
         kc, vc = (torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16) for _ in range(2))
