@@ -348,7 +348,7 @@ def _check_varlen(o, lse, q, kc, vc, table, seq_lens, starts, qlens, causal, dty
 
 
 @pytest.mark.parametrize("route,bs,causal", [("single", 64, True), ("split", 64, True), ("split", 16, True),
-                                             ("single", 128, False)])
+                                             ("single", 128, False), ("single", 16, True), ("single", 4, False)])
 def test_paged_variable_query_lengths(route, bs, causal):
     from gqa_kernels.paged import paged_attention
     Hq, Hkv, D = 32, 8, 128
