@@ -73,8 +73,9 @@ const char* gqa_strerror(int code) {
     case GQA_E_GROUP: return "group size (num_heads / num_kv_heads) larger than 256";
     case GQA_E_NULL: return "null pointer argument";
     case GQA_E_BLOCK:
-      return "paged cache: block_size must be a power of two in [1, GQA_MAX_BLOCK_SIZE] and "
-             "table_stride * block_size must cover max_seq_len";
+      return "paged cache: block_size must be a power of two in [1, GQA_MAX_BLOCK_SIZE] "
+             "(gqa_paged_fwd_launch: >= 512 / head_dim) and table_stride * block_size must cover "
+             "max_seq_len";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

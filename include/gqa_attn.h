@@ -48,7 +48,8 @@ extern "C" {
 #define GQA_E_GROUP (-6)      /* group size above what one packed tile holds */
 #define GQA_E_NULL (-7)       /* null pointer argument */
 #define GQA_E_BLOCK (-8)      /* paged cache: block_size not a power of two in
-                                 [1, GQA_MAX_BLOCK_SIZE], or table too short */
+                                 [1, GQA_MAX_BLOCK_SIZE] (single pass: below
+                                 512 / head_dim), or table too short */
 
 #define GQA_MAX_SPLITS 1024
 #define GQA_MAX_BLOCK_SIZE 65536
