@@ -334,13 +334,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ ST::sv(lrow));
 
   // Issue this wave's share of K or V tile `tile` (absolute index) into LDS.
-  // Paged: the tile's 64 rows are one run inside one block; its descriptor
-  // starts at the tile's first row and ends at the sequence's last key, so
-  // rows past the sequence (and whole tiles past it, which read no table
-  // entry) load as zeros.
-  // Paged: the block holding a tile (read only for tiles that start inside
-  // the sequence).  The softmax phases use a block id read one phase ahead
-  // (blk_next), so the table read's latency is off the issue path.
+  // Paged, blocks of >= 64 keys: the tile's 64 rows are one run inside one
+  // block; its descriptor starts at the tile's first row and ends at the
+  // sequence's last key, so rows past the sequence (and whole tiles past it,
+  // which read no table entry) load as zeros.  Smaller blocks: the same per
+  // LDS-DMA instruction (RPI rows, one run inside one block).
+  // Paged: the block(s) holding a tile, or this wave's instructions of it
+  // (read only for rows that start inside the sequence).  The softmax phases
+  // use block ids read one phase ahead (blk_next), so the table reads'
+  // latency is off the issue path.
   auto tile_block = [&](int tile) -> TileBlocks {
     TileBlocks tbk;
     const int key0 = tile * ST::kKeys;
