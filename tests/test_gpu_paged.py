@@ -367,14 +367,16 @@ def test_paged_variable_query_lengths(route, bs, causal):
     _check_varlen(o.cpu(), lse.cpu(), q, kc, vc, table, seq_lens, starts, qlens, causal, dt)
 
 
-def test_vllm_shaped_layer_mixed_batch():
+@pytest.mark.parametrize("bs", [64, 16])
+def test_vllm_shaped_layer_mixed_batch(bs):
     """Prefill chunks and decode steps in one call: the layer runs one launch
-    per kernel route over token-major views."""
+    per kernel route over token-major views (16-key blocks: both routes on
+    blocks under one 64-key tile)."""
     from gqa_kernels.paged import GQAPagedAttention, PagedAttentionMetadata, PagedKVCache
-    Hq, Hkv, D, bs = 32, 8, 128, 64
+    Hq, Hkv, D = 32, 8, 128
     dt = torch.bfloat16
     g = torch.Generator().manual_seed(17)
-    cache = PagedKVCache(300, bs, Hkv, D, dtype=dt, device=DEV)
+    cache = PagedKVCache(300 * 64 // bs, bs, Hkv, D, dtype=dt, device=DEV)
     layer = GQAPagedAttention(Hq, D, num_kv_heads=Hkv)
     hist = {}
     for s, n in enumerate([1200, 0, 3000, 55]):  # sequence 1 starts empty (a fresh prompt)
