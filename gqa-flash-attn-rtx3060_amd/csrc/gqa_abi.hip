@@ -16,7 +16,10 @@ namespace {
 using gqa::Dims;
 using gqa::TensorRef;
 
-constexpr int kAbiVersion = 6;
+// 7: gqa_paged_split_first_launch limits a chunk over pages of < 64 keys to
+// GQA_PAGED_CHUNK_PAGES pages (GQA_E_SPLITS beyond); a sequence without keys
+// gives zero rows on every path.
+constexpr int kAbiVersion = 7;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;

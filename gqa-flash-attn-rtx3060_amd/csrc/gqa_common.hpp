@@ -177,15 +177,17 @@ struct ContigRows {
 template <typename T, bool kBigPages>
 struct PagedRows {
   const T* base;      // the cache at this kv head (block 0, slot 0)
-  const int* table;   // this sequence's row of the block table
+  const int* table;   // this sequence's block-table entries from page tab0 on
   int64_t sblk, sss;  // block and slot strides (elements)
   int shift;          // log2(block_size)
+  int tab0;           // page index of table[0] (a slice of the row staged in LDS)
   __device__ const T* row(int key) const {
-    return base + (int64_t)table[key >> shift] * sblk + (int64_t)(key & ((1 << shift) - 1)) * sss;
+    return base + (int64_t)table[(key >> shift) - tab0] * sblk + (int64_t)(key & ((1 << shift) - 1)) * sss;
   }
   // The same for a key that is equal in every lane (scalar table read).
   __device__ const T* row_uniform(int key) const {
-    return base + (int64_t)load_uniform(table + (key >> shift)) * sblk + (int64_t)(key & ((1 << shift) - 1)) * sss;
+    return base + (int64_t)load_uniform(table + ((key >> shift) - tab0)) * sblk +
+           (int64_t)(key & ((1 << shift) - 1)) * sss;
   }
   __device__ static constexpr bool run64() { return kBigPages; }
 };

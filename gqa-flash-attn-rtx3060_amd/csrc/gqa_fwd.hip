@@ -681,12 +681,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     m_run = mm;
   }
 
-  // Epilogue: o = acc / l (0/0 = NaN for a row with no visible key, as the
-  // reference's acc / l_i at gqa_fwd.py:106).  Optional LSE side output:
-  // ln sum_k exp(s_k * D^-0.5) = (m_ref * c + log2 l) * ln 2 (l is relative
-  // to the reference point m_ref); -inf for a row with no visible key.
+  // Epilogue: o = acc / l (0/0 = NaN for a row whose keys are all masked, as
+  // the reference's acc / l_i at gqa_fwd.py:106).  A sequence with no keys
+  // at all gives zero rows instead: tests/reference.py:33-34 takes the
+  // softmax over an empty key axis and multiplies it with an empty V.
+  // Optional LSE side output: ln sum_k exp(s_k * D^-0.5) = (m_ref * c +
+  // log2 l) * ln 2 (l is relative to the reference point m_ref); -inf for a
+  // row with no visible key.
   const float l_tot = xhalf_sum(l_run);
-  const float inv = 1.0f / l_tot;
+  const float inv = skv == 0 ? 0.f : 1.0f / l_tot;
   if (p.lse != nullptr && valid && hh == 0) {
     // (B, Hq, Sq), or (tokens, Hq) with variable lengths.
     const int64_t li = varlen ? (tok0 + pos) * dm.Hq + head : ((int64_t)b * dm.Hq + head) * dm.Sq + pos;

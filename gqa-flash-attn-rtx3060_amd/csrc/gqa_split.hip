@@ -18,6 +18,9 @@
 // Combine: one workgroup per (batch, q head, row):
 //   m* = max m_s, a_s = exp2(m_s - m*), l* = sum a_s l_s,
 //   o = sum a_s acc_s / l*                         (gqa_split.py:134-147)
+// Rows whose keys are all masked give NaN (m* = -inf), as the reference's
+// combine; rows of a sequence with no keys at all (first pass stores m = 0,
+// l = 0: a finite m* with l* = 0) give zeros, as tests/reference.py:33-34.
 //
 // Paged variants (KV = 1, 2; no counterpart in the reference): the same
 // first pass over a (num_blocks, block_size, Hkv, D) cache, with each
@@ -116,7 +119,8 @@ __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb
     const int d4 = f % NDP, rl = f / NDP;
     f32x4 o = red[f];
     for (int sg = 1; sg < nsg; ++sg) o += red[sg * R * NDP + f];
-    const float l = lst[rl];
+    // A sequence without keys (finite m*, l* = 0, o = 0): 0 / inf = 0.
+    const float l = (lst[rl] == 0.f && mst[rl] > -__builtin_inff()) ? __builtin_inff() : lst[rl];
     const int r = r0 + rl;
     const int pos = r / dm.G, g = r - pos * dm.G;
     T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb +
@@ -202,6 +206,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   Rows kr, vr;
   if constexpr (PAGED) {
     const int* table = p.block_table + (int64_t)b * p.table_stride;
+    int tab0 = 0;
     if constexpr (KV == 2) {
       // Pages under 64 keys: every key row resolves its own page, so the
       // chunk's slice of the block table is copied to LDS once and the
@@ -213,10 +218,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int np = c1 > c0 ? ((c1 - 1) >> p.block_shift) - p0 + 1 : 0;
       for (int e = t; e < np && e < kPagedTableMax; e += 256) s_tab[e] = table[p0 + e];
       __syncthreads();
-      table = s_tab - p0;
+      table = s_tab;  // entry e = page p0 + e
+      tab0 = p0;
     }
-    kr = Rows{static_cast<const T*>(p.k.ptr) + (int64_t)kvh * p.k.sh, table, p.k.sb, p.k.ss, p.block_shift};
-    vr = Rows{static_cast<const T*>(p.v.ptr) + (int64_t)kvh * p.v.sh, table, p.v.sb, p.v.ss, p.block_shift};
+    kr = Rows{static_cast<const T*>(p.k.ptr) + (int64_t)kvh * p.k.sh, table, p.k.sb, p.k.ss, p.block_shift, tab0};
+    vr = Rows{static_cast<const T*>(p.v.ptr) + (int64_t)kvh * p.v.sh, table, p.v.sb, p.v.ss, p.block_shift, tab0};
   } else {
     kr = Rows{static_cast<const T*>(p.k.ptr) + (int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh, p.k.ss};
     vr = Rows{static_cast<const T*>(p.v.ptr) + (int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh, p.v.ss};
@@ -365,8 +371,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) store_coherent(wa + 32 * db + 8 * j + 4 * hh + e, o[j][e]);
+      // A sequence without keys stores m = 0, l = 0 (never produced
+      // otherwise: the chunk's largest score contributes exp2(0) = 1 to l),
+      // which the combine turns into a zero row.
       if (db == 0 && hh == 0) {
-        store_coherent(p.ws_m + row, mstar * c);
+        store_coherent(p.ws_m + row, skv == 0 ? 0.f : mstar * c);
         store_coherent(p.ws_l + row, lsum);
       }
     }
@@ -456,6 +465,8 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
     T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) +
               (varlen ? tok * p.o.ss + (int64_t)h * p.o.sh
                       : (int64_t)b * p.o.sb + (int64_t)h * p.o.sh + (int64_t)pos * p.o.ss);
+    // A sequence without keys (finite m*, l* = 0, o = 0): 0 / inf = 0.
+    if (l == 0.f && mstar > -__builtin_inff()) l = __builtin_inff();
     u32x2 x;
     x[0] = E::pack2(o[0] / l, o[1] / l);
     x[1] = E::pack2(o[2] / l, o[3] / l);

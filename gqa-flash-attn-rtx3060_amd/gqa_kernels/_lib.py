@@ -19,7 +19,7 @@ DTYPE_FP16 = 1
 GQA_MAX_SPLITS = 1024
 GQA_MAX_BLOCK_SIZE = 65536
 GQA_PAGED_CHUNK_PAGES = 2048
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3

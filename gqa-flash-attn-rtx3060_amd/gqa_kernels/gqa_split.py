@@ -30,6 +30,12 @@ _counters_lock = threading.Lock()
 # allocator would hand out the same memory anyway; keeping it saves the
 # allocation on every decode step.)
 _workspaces: dict = {}
+# Buffers replaced by a larger one.  A CUDA/HIP graph captured while a buffer
+# was current keeps its raw address and writes to it on every replay, so a
+# superseded buffer is never released: it stays here for the life of the
+# process.  Each replacement at least doubles the size, so everything kept is
+# less than the current buffer again.
+_retired: list = []
 
 
 # The current stream's raw handle: one C call, where torch.cuda.current_stream()
@@ -49,7 +55,11 @@ def _workspace_buffer(device: torch.device, stream: int, nbytes: int) -> torch.T
     with _counters_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() * 4 < nbytes:
-            buf = torch.empty(max(nbytes // 4, 1 << 16), dtype=torch.float32, device=device)
+            n = max(-(-nbytes // 4), 1 << 16)
+            if buf is not None:
+                _retired.append(buf)  # a captured graph may still write to it
+                n = max(n, 2 * buf.numel())
+            buf = torch.empty(n, dtype=torch.float32, device=device)
             _workspaces[key] = buf
         return buf
 
@@ -59,7 +69,11 @@ def _counter_buffer(device: torch.device, stream: int, n: int) -> torch.Tensor:
     with _counters_lock:
         buf = _counters.get(key)
         if buf is None or buf.numel() < n:
-            buf = torch.zeros(max(n, 1024), dtype=torch.int32, device=device)
+            m = max(n, 1024)
+            if buf is not None:
+                _retired.append(buf)  # a captured graph may still count in it
+                m = max(m, 2 * buf.numel())
+            buf = torch.zeros(m, dtype=torch.int32, device=device)
             _counters[key] = buf
         return buf
 

@@ -98,9 +98,15 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
            and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
         splits *= 2
     if block_size < 64:
-        while (paged_chunk(max_seq_len, splits) // block_size > _lib.GQA_PAGED_CHUNK_PAGES
-               and splits < _lib.GQA_MAX_SPLITS):
+        def too_many_pages(s):
+            return paged_chunk(max_seq_len, s) // block_size > _lib.GQA_PAGED_CHUNK_PAGES
+        while too_many_pages(splits) and splits < _lib.GQA_MAX_SPLITS:
             splits *= 2
+        if too_many_pages(splits):
+            raise ValueError(
+                f"paged split-KV: max_seq_len {max_seq_len} over {block_size}-key blocks needs chunks of at "
+                f"most {_lib.GQA_PAGED_CHUNK_PAGES} blocks, more than {_lib.GQA_MAX_SPLITS} splits give; "
+                f"use blocks of >= 64 keys or a shorter max_seq_len")
     return splits
 
 

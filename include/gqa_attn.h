@@ -55,7 +55,11 @@ extern "C" {
 #define GQA_MAX_BLOCK_SIZE 65536
 #define GQA_PAGED_CHUNK_PAGES 2048 /* pages per split chunk when block_size < 64 */
 
-/* ABI revision; bumped when a signature below changes. */
+/* ABI revision; bumped when a signature or a documented limit below
+ * changes.  7: a paged split chunk over pages of fewer than 64 keys may span
+ * at most GQA_PAGED_CHUNK_PAGES pages (GQA_E_SPLITS beyond), and a sequence
+ * without keys (seq_kv = 0, or seq_lens[b] = 0) gives zero output rows and
+ * LSE -inf on every path. */
 int gqa_abi_version(void);
 
 /* Message for a return code (GQA_E* or hipError_t).  Never NULL. */

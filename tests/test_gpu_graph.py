@@ -70,6 +70,55 @@ def test_public_path_in_graph(case):
     _replays(g, out, expect)
 
 
+def test_graph_workspace_outlives_growth():
+    """A decode graph keeps the raw address of the split workspace it was
+    captured with.  A later, larger call on the same stream (a 1024-token
+    prefill with the key split) replaces the stream's cached workspace; the
+    replaced buffer must stay allocated, or the decode replays would write
+    their partials into memory handed to other tensors.  Both calls warm up
+    eagerly on the capture stream (so the first workspace comes from the
+    general pool), the captures share one memory pool (vLLM's pattern), and
+    tensors allocated afterwards at the first workspace's size must keep
+    their contents across replays."""
+    from gqa_kernels import gqa_flash_attn, gqa_split
+    from gqa_kernels.dispatch import _cu_count, choose_route
+    qd, kd, vd = make_inputs(1, 32, 8, 1, 16384, 128, torch.bfloat16, seed=31, device=DEV)
+    qp, kp, vp = make_inputs(1, 32, 8, 1024, 1024, 128, torch.bfloat16, seed=32, device=DEV)
+    assert choose_route(1, 32, 8, 1024, 1024, _cu_count(0)).fwd_split > 0
+    dec = lambda: gqa_flash_attn(qd, kd, vd, causal=True)
+    pre = lambda: gqa_flash_attn(qp, kp, vp, causal=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        exp_d = dec().clone()
+    torch.cuda.synchronize()
+    key = (torch.device(DEV).index or 0, s.cuda_stream)
+    ws_dec = gqa_split._workspaces[key]
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1, stream=s):
+        out_d = dec()
+    with torch.cuda.stream(s):
+        exp_p = pre().clone()  # grows the stream's workspace
+    torch.cuda.synchronize()
+    assert gqa_split._workspaces[key].data_ptr() != ws_dec.data_ptr()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=s, pool=g1.pool()):
+        out_p = pre()
+    n = ws_dec.numel()
+    del ws_dec
+    fills = [torch.full((n,), float(i + 1), device=DEV) for i in range(6)]
+    torch.cuda.synchronize()
+    for i in range(3):
+        g1.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_d, exp_d), f"decode replay {i} differs from eager"
+        for j, f in enumerate(fills):
+            assert bool((f == j + 1).all()), f"decode replay {i} wrote into a fresh tensor"
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_p, exp_p), f"prefill replay {i} differs from eager"
+
+
 def test_fused_split_in_graph():
     from gqa_kernels.gqa_split import split_kv_forward
     q, k, v = make_inputs(1, 32, 8, 1, 8192, 128, torch.bfloat16, seed=3, device=DEV)

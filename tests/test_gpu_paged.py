@@ -57,6 +57,9 @@ def _paged_inputs(B, Hq, Hkv, Sq, lens, D, block_size, dtype, seed, spare_blocks
 def _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype):
     ref_o, ref_lse = paged_reference(to_np(q), to_np(kc), to_np(vc), table.numpy(), seq_lens.numpy(), causal)
     got = to_np(o)
+    # A sequence without keys: zero rows (tests/reference.py:33-34 over an
+    # empty key axis), exactly.
+    assert np.all(got[seq_lens.numpy() == 0] == 0) and np.all(ref_o[seq_lens.numpy() == 0] == 0)
     nan = np.isnan(ref_o)
     assert np.array_equal(np.isnan(got), nan), "fully masked rows differ"
     assert_close(got[~nan], ref_o[~nan], BASELINE_TOL[dtype], "paged")
@@ -75,6 +78,7 @@ def _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype):
     (2, 32, 8, 3, [2, 900], 64, 8, torch.float16, True),                  # seq shorter than Sq: masked rows
     (2, 32, 4, 16, [1500, 260], 64, 256, torch.bfloat16, False),          # chunk, non-causal, big pages
     (1, 16, 16, 1, [333], 128, 1, torch.bfloat16, True),                  # MHA, one-slot pages
+    (3, 32, 8, 1, [0, 500, 64], 128, 16, torch.bfloat16, True),           # a sequence without keys: zeros
 ])
 def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal):
     from gqa_kernels.paged import paged_attention
@@ -102,6 +106,7 @@ def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, caus
     (2, 32, 8, 90, [999, 400], 128, 32, torch.float16, False, True),         # 32-key blocks, fp16
     (2, 16, 4, 70, [701, 333], 64, 8, torch.float16, True, False),           # smallest block at D = 64
     (1, 16, 2, 120, [1500], 64, 16, torch.bfloat16, False, True),            # D = 64, 16-key HND
+    (2, 32, 8, 100, [0, 700], 128, 64, torch.bfloat16, True, False),         # a sequence without keys: zeros
 ])
 def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal, hnd):
     """Query blocks above the split-KV size take the single-pass kernel with
@@ -121,12 +126,17 @@ def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, ca
     _check(o_split, None, q, kc, vc, table, seq_lens, causal, dtype)
 
 
-def test_paged_single_pass_equals_contiguous_prefill_chunk():
+@pytest.mark.parametrize("D,bs", [(128, 128), (128, 16), (128, 4), (64, 8)])
+def test_paged_single_pass_equals_contiguous_prefill_chunk(D, bs):
     """The chunked-prefill BASELINE shape (B=4, 512 new tokens over 8192 keys)
-    from a shuffled 128-key-block cache vs the contiguous single pass."""
+    from a shuffled block cache vs the contiguous single pass: bit-identical
+    for blocks of whole tiles (128) and for blocks under a tile, where every
+    LDS-DMA instruction gets its own descriptor (16, and 4 / 8: the fewest
+    rows one instruction loads at D = 128 / 64)."""
     from gqa_kernels import gqa_flash_attn
     from gqa_kernels.paged import paged_attention
-    B, Hq, Hkv, Sq, L, D, bs = 4, 32, 8, 512, 8192, 128, 128
+    B, Hq, Hkv, Sq, L = 4, 32, 8, 512, 8192
+    print(f"paged == contiguous D={D} bs={bs}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(21)
     q = torch.randn(B, Hq, Sq, D, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(B, Hkv, L, D, generator=g, device=DEV).to(torch.bfloat16)

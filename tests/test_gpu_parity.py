@@ -350,3 +350,46 @@ def test_empty_query():
     q, k, v = make_inputs(1, 8, 2, 0, 64, 128, device=DEV)
     out = _run(q, k, v)
     assert out.shape == (1, 8, 0, 128)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,D", [(1, 32, 8, 1, 128), (1, 32, 8, 17, 128), (2, 8, 2, 300, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_empty_cache_gives_zeros(B, Hq, Hkv, Sq, D, causal):
+    """seq_kv = 0: tests/reference.py:33-34 takes the softmax over an empty
+    key axis and multiplies it by an empty V, which gives zero rows (the
+    oracle restates that).  Every route returns exact zeros and LSE -inf."""
+    from gqa_kernels.gqa_split import split_kv_forward
+    q, k, v = make_inputs(B, Hq, Hkv, Sq, 0, D, device=DEV)
+    ref = oracle(q, k, v, causal)
+    assert ref.shape == tuple(q.shape) and np.all(ref == 0)
+    zeros = torch.zeros_like(q)
+    out, lse = _attn()(q, k, v, causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, zeros) and bool(torch.isneginf(lse).all())
+    for fused in (False, True):  # the split-KV kernels, called directly
+        for S in (1, 4):
+            o2, lse2 = split_kv_forward(q, k, v, causal, S, fused=fused, return_lse=True)
+            torch.cuda.synchronize()
+            assert torch.equal(o2, zeros), (fused, S)
+            assert bool(torch.isneginf(lse2).all()), (fused, S)
+
+
+@pytest.mark.parametrize("route", ["split", "single"])
+def test_cpu_baseline_config_unit_normal(route):
+    """BASELINE configs[0], the reference's CPU config, on the GPU: decode
+    B=1, Hq=32, Hkv=8, D=128, seq_kv=2048, causal, q/k/v ~ N(0,1) drawn in
+    that order from a CPU generator with seed 0 (the inputs bench.py's
+    cpu_baseline times), at the BASELINE gate max abs <= 2e-2, mean abs
+    <= 2e-3 — through the split-KV route the dispatch picks and through the
+    single-pass kernel."""
+    from gqa_kernels.dispatch import single_pass_forward
+    q, k, v = make_inputs(1, 32, 8, 1, 2048, 128, seed=0, device=DEV)
+    assert _route(q, k).kind == "split"
+    if route == "split":
+        out = _run(q, k, v)
+    else:
+        out = single_pass_forward(q, k, v, torch.empty_like(q), True)
+        torch.cuda.synchronize()
+    ref = oracle(q, k, v)
+    mx, mn = assert_close(out, ref, BASELINE_TOL[torch.bfloat16], f"CPU-baseline config, {route} route")
+    print(f"cpu-baseline config {route}: max abs {mx:.3e} mean abs {mn:.3e}", flush=True)

@@ -229,6 +229,20 @@ def test_fully_masked_rows_nan():
     del t
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_empty_cache_is_zero(causal):
+    # seq_kv = 0: reference.py:25-34 multiplies the softmax over an empty key
+    # axis (an empty (Sq, 0) matrix; the mask changes nothing) by an empty V,
+    # which torch evaluates to zeros, and so does the oracle; the LSE over no
+    # keys is -inf.
+    q, k, v = _rand(2, 4, 2, 3, 0, 8, seed=8)
+    w = torch.softmax(torch.empty(3, 0, dtype=torch.float64), dim=-1)
+    assert torch.equal(w @ torch.empty(0, 8, dtype=torch.float64), torch.zeros(3, 8, dtype=torch.float64))
+    o = O.gqa_reference(q, k, v, causal, dtype=np.float64)
+    assert o.shape == (2, 4, 3, 8) and np.all(o == 0)
+    assert np.isneginf(O.gqa_lse(q, k, v, causal)).all()
+
+
 def test_split_partials_empty_chunks():
     # Chunks with no visible key: m = -inf, l = 0, acc = 0 (gqa_split.py:79-81).
     q, k, v = _rand(1, 2, 1, 10, 12, 4, seed=6)

@@ -243,6 +243,11 @@ def test_paged_splits_small_pages():
                 s = paged_splits(B, 32, 8, 1, L, 256, block_size=bs)
                 assert s & (s - 1) == 0 and s <= _lib.GQA_MAX_SPLITS
                 assert paged_chunk(L, s) // bs <= _lib.GQA_PAGED_CHUNK_PAGES
+    # GQA_MAX_SPLITS chunks of at most 2048 one-key pages cover 2^21 keys:
+    # beyond that no split count fits, and the error says why.
+    assert paged_splits(1, 32, 8, 1, 1 << 21, 256, block_size=1) == _lib.GQA_MAX_SPLITS
+    with pytest.raises(ValueError, match="2048 blocks"):
+        paged_splits(1, 32, 8, 1, (1 << 21) + 64, 256, block_size=1)
 
 
 # ---------------------------------------------------------------------------
