@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "../../include/gqa_attn.h"
 #include "gqa_params.hpp"
@@ -18,8 +20,8 @@ using gqa::TensorRef;
 
 // 7: gqa_paged_split_first_launch limits a chunk over pages of < 64 keys to
 // GQA_PAGED_CHUNK_PAGES pages (GQA_E_SPLITS beyond); a sequence without keys
-// gives zero rows on every path.
-constexpr int kAbiVersion = 7;
+// gives zero rows on every path.  8: gqa_split_noalloc_launch.
+constexpr int kAbiVersion = 8;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -79,6 +81,10 @@ const char* gqa_strerror(int code) {
       return "paged cache: block_size must be a power of two in [1, GQA_MAX_BLOCK_SIZE] "
              "(gqa_paged_fwd_launch: >= 512 / head_dim) and table_stride * block_size must cover "
              "max_seq_len";
+    case GQA_E_SCRATCH:
+      return "gqa_split_noalloc_launch: the split partials exceed its fixed buffer "
+             "(GQA_NOALLOC_SCRATCH_BYTES, 16 MiB); use fewer splits or gqa_split_first_launch with a "
+             "caller workspace";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -505,4 +511,67 @@ int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_str
   return to_code(gqa::launch_split_reduce(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+// ---------------------------------------------------------------------------
+// The fixed partials buffer of gqa_split_noalloc_launch.  The runtime gives
+// every device its own copy when it loads this code object; it is held until
+// the process ends.  In host code `scratch` names a host-side stand-in, not
+// device memory: only the address hipGetSymbolAddress returns for the
+// current device may reach a kernel, memset or copy.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchFloats = GQA_NOALLOC_SCRATCH_BYTES / sizeof(float);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's copy of `scratch`, looked up once
+// per device with that device current.
+int scratch_address(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return static_cast<int>(hipErrorInvalidDevice);
+  float* a = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (a == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    a = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (a == nullptr) {
+      void* sym = nullptr;
+      e = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (sym == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+      a = static_cast<float*>(sym);
+      g_scratch_addr[dev].store(a, std::memory_order_release);
+    }
+  }
+  *out = a;
+  return GQA_OK;
+}
+
 }  // namespace
+
+extern "C" {
+
+int gqa_split_noalloc_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                             const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
+                             float* lse, int splits, int batch, int num_heads, int num_kv_heads, int seq_q,
+                             int seq_kv, int head_dim, float scale_log2, int causal, int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
+  if (rc) return rc;
+  if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (gqa_split_workspace_bytes(batch, num_heads, seq_q, head_dim, splits) > GQA_NOALLOC_SCRATCH_BYTES)
+    return GQA_E_SCRATCH;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  // o is checked before the first pass is enqueued (q, k, v by the first pass).
+  if ((rc = check_tensor(o, o_stride))) return rc;
+  float* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  rc = gqa_split_first_launch(q, q_stride, k, k_stride, v, v_stride, ws, splits, batch, num_heads, num_kv_heads,
+                              seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
+  if (rc) return rc;
+  return reduce_impl(ws, splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream);
+}
+
+}  // extern "C"

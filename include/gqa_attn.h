@@ -50,6 +50,8 @@ extern "C" {
 #define GQA_E_BLOCK (-8)      /* paged cache: block_size not a power of two in
                                  [1, GQA_MAX_BLOCK_SIZE] (single pass: below
                                  512 / head_dim), or table too short */
+#define GQA_E_SCRATCH (-9)    /* gqa_split_noalloc_launch: partials larger than
+                                 GQA_NOALLOC_SCRATCH_BYTES */
 
 #define GQA_MAX_SPLITS 1024
 #define GQA_MAX_BLOCK_SIZE 65536
@@ -193,6 +195,32 @@ int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4],
                                int seq_q, int seq_kv, int head_dim,
                                float scale_log2, int causal, int dtype,
                                void* stream);
+
+/* Split-KV forward that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory or hand in a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  It runs gqa_split_first_launch and then
+ * gqa_split_reduce_launch (gqa_split_reduce_lse_launch when lse is not
+ * NULL) on `stream`, with the fp32 partials in a fixed buffer inside the
+ * library instead of a caller workspace; q, k, v, o and lse are the
+ * caller's, as there.
+ * Limit: gqa_split_workspace_bytes(batch, num_heads, seq_q, head_dim, splits)
+ * must be at most GQA_NOALLOC_SCRATCH_BYTES (16 MiB: e.g. 64 splits of a
+ * decode step of 64 query heads at batch 16), else GQA_E_SCRATCH, before any
+ * HIP call.  The buffer exists once per device, for the life of the
+ * process, and every call on that device shares it: calls that can overlap
+ * on one device (different streams, or two host threads) race on it and must
+ * use gqa_split_first_launch with workspaces of their own.  The pointers and
+ * the stream must belong to the current device. */
+#define GQA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int gqa_split_noalloc_launch(const void* q, const int64_t q_stride[4],
+                             const void* k, const int64_t k_stride[4],
+                             const void* v, const int64_t v_stride[4],
+                             void* o, const int64_t o_stride[4], float* lse,
+                             int splits, int batch, int num_heads, int num_kv_heads,
+                             int seq_q, int seq_kv, int head_dim,
+                             float scale_log2, int causal, int dtype,
+                             void* stream);
 
 /* Paged KV cache.  The reference names a persistent prefix KV cache and a
  * vLLM-shaped interface as the next step after its kernel (README.md:140-146,
