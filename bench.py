@@ -5,10 +5,15 @@ Prints ONE JSON line (rank 0).  The headline ``value`` is causal-prefill
 TFLOP/s at the Llama-3.1-8B GQA shape, seq 16384 (B=1, Hq=32, Hkv=8, D=128,
 bf16); the ``decode`` object carries split-KV decode at seq_kv 131072
 (microseconds and HBM GB/s), ``paged_decode`` the same decode over a paged
-KV cache (gqa_kernels.paged) at two block sizes / in-block layouts, and
-``paged_prefill`` the chunked-prefill shape over a paged cache.  Timing follows reference benchmark/run.py:140-154
-(untimed warm-up calls, then back-to-back calls of the full public function
-between two events on the launch stream, mean per call).
+KV cache (gqa_kernels.paged) at two block sizes / in-block layouts,
+``paged_prefill`` the chunked-prefill shape over a paged cache, and
+``configs`` every BASELINE config (prefill 2048-16384, decode 2048-131072,
+chunked prefill, the 70B decode shape) with its time and the fraction of the
+roofline (MFMA or HBM) that bounds it; HBM-bound configs rotate K/V sets so
+the Infinity Cache cannot serve a call from the previous one.  Timing
+follows reference benchmark/run.py:140-154 (untimed warm-up calls, then
+back-to-back calls of the full public function between two events on the
+launch stream, mean per call).
 
 Work counts (algorithmic, implementation overhead excluded):
   FLOPs = 4 * D * B * Hq * visible (query, key) pairs
@@ -18,7 +23,7 @@ Work counts (algorithmic, implementation overhead excluded):
 reference's torch oracle, the reference's only CPU path) on a bounded sample
 of the same prefill workload, on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--sweep]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only WORKLOAD]
 """
 from __future__ import annotations
 
@@ -241,13 +246,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
-    ap.add_argument("--sweep", action="store_true", help="also time every BASELINE config")
-    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b"],
+    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b", "configs"],
                     default=None,
                     help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
                          "device copy, the calibration kernel of the HBM traffic counters; 'gemm' "
                          "a 16384^3 bf16 library GEMM, the practical MFMA ceiling of the box; "
-                         "'chunked' and '70b' one BASELINE config of the sweep each")
+                         "'chunked' and '70b' one BASELINE config each; 'configs' every BASELINE config")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -347,10 +351,14 @@ def main() -> int:
         result["paged_prefill"] = paged_prefill(torch, args.steps, args.warmup)
         torch.cuda.empty_cache()
 
-    if args.sweep:
-        result["sweep"] = sweep(torch, gqa_flash_attn)
-    if args.only in ("chunked", "70b"):
-        result["sweep"] = sweep(torch, gqa_flash_attn, only=args.only)
+    # ---------------- every BASELINE config ----------------
+    if args.only is None:
+        result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup)
+    elif args.only in ("chunked", "70b"):
+        result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup,
+                                  only={"chunked": "chunked", "70b": "70B"}[args.only])
+    elif args.only == "configs":
+        result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup)
 
     if result["value"] is None and "decode" in result:
         d = result["decode"]
@@ -419,24 +427,48 @@ def paged_prefill(torch, steps, warmup):
     return out
 
 
-def sweep(torch, gqa_flash_attn, only=None):
-    """Every BASELINE config (or the one named `only`): mean ms over 20 calls
-    after 5 warm-ups."""
-    cfgs = [("prefill", 1, 32, 8, s, s) for s in (2048, 4096, 8192, 16384)]
-    cfgs += [("decode", 1, 32, 8, 1, s) for s in (8192, 32768, 131072)]
-    cfgs += [("chunked", 4, 32, 8, 512, 8192), ("70b", 16, 64, 8, 4, 32768)]
-    if only is not None:
-        cfgs = [c for c in cfgs if c[0] == only]
+# Every BASELINE config (BASELINE.json "configs"): name, B, Hq, Hkv, seq_q,
+# seq_kv and the roofline that bounds it.  configs[0] is the reference's CPU
+# config (decode at 2048 keys), here timed on the GPU beside its CPU time.
+CONFIGS = (
+    [("cpu-config decode 2048", 1, 32, 8, 1, 2048, "hbm")]
+    + [(f"prefill {s}", 1, 32, 8, s, s, "mfma") for s in (2048, 4096, 8192, 16384)]
+    + [(f"decode {s}", 1, 32, 8, 1, s, "hbm") for s in (8192, 32768, 131072)]
+    + [("chunked prefill B=4 512/8192", 4, 32, 8, 512, 8192, "mfma"),
+       ("70B decode B=16 Hq=64 Sq=4 32768", 16, 64, 8, 4, 32768, "hbm")]
+)
+# K/V sets rotated per HBM-bound config: enough that consecutive calls cannot
+# find the previous calls' keys in the 256 MB Infinity Cache.
+ROTATE_BYTES = 600e6
+
+
+def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None):
+    """Time every BASELINE config (or the ones whose name starts with
+    `only`): mean µs over `steps` back-to-back calls (5x as many for
+    HBM-bound configs, which take microseconds) after `warmup` calls, with
+    TFLOP/s, HBM GB/s and the fraction of the roofline that bounds the
+    config.  HBM-bound configs rotate K/V sets (ROTATE_BYTES in total)."""
+    from gqa_kernels.dispatch import _cu_count, choose_route
     rows = []
-    for name, b, hq, hkv, sq, skv in cfgs:
+    for name, b, hq, hkv, sq, skv, bound in CONFIGS:
+        if only is not None and not name.startswith(only):
+            continue
         by1 = hbm_bytes(b, hq, hkv, sq, skv, D)
-        nset = 1 if by1 > 600e6 else max(2, math.ceil(600e6 / by1))
-        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, D, n_kv_sets=min(nset, 8))
-        ms = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % len(kvs)], causal=True), 20, 5)
+        nset = max(1, math.ceil(ROTATE_BYTES / by1)) if bound == "hbm" else 1
+        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, D, seed=len(rows) + 11, n_kv_sets=nset)
+        n = steps * 5 if bound == "hbm" else steps
+        ms = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % nset], causal=True), n, warmup)
         fl = flops(b, hq, sq, skv, D)
-        rows.append({"workload": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv,
-                     "ms": ms, "tflops": fl / (ms * 1e-3) / 1e12,
-                     "gbs": by1 / (ms * 1e-3) / 1e9})
+        tflops, gbs = fl / (ms * 1e-3) / 1e12, by1 / (ms * 1e-3) / 1e9
+        achieved, peak, unit = (tflops, PEAK_BF16_TFLOPS, "TFLOP/s") if bound == "mfma" else \
+            (gbs, PEAK_HBM_GBS, "GB/s")
+        route = choose_route(b, hq, hkv, sq, skv, _cu_count(0))
+        rows.append({"config": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv, "D": D,
+                     "us": ms * 1e3, "tflops": tflops, "gbs": gbs, "steps": n, "kv_sets": nset,
+                     "route": route.kind + (f" splits={route.splits}" if route.kind == "split" else
+                                            f" key-split blocks={route.fwd_split}" if route.fwd_split else ""),
+                     "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                                  "frac": achieved / peak, "flops_per_call": fl, "bytes_per_call": by1}})
         del q, kvs
         torch.cuda.empty_cache()
     return rows

@@ -120,21 +120,32 @@ def correctness_check(torch, gqa_flash_attn, dtype, gen):
 
 
 def _time(torch, fn):
-    """Mean ms per call over ITERS back-to-back calls after WARMUP (reference
-    run.py:144-158), and the peak memory allocated meanwhile (GB)."""
+    """Mean ms per call over ITERS back-to-back calls fn(0), fn(1), ...
+    after WARMUP (reference run.py:144-158), and the peak memory allocated
+    meanwhile (GB)."""
     torch.cuda.synchronize()
-    for _ in range(WARMUP):
-        fn()
+    for i in range(WARMUP):
+        fn(i)
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(ITERS):
-        fn()
+    for i in range(ITERS):
+        fn(i)
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / ITERS, torch.cuda.max_memory_allocated() / (1024 ** 3)
+
+
+# Decode rows read each K/V byte once per call, so back-to-back calls on one
+# K/V set would be served by the 256 MB Infinity Cache, not HBM: they rotate
+# through as many sets as it takes to stream at least this many bytes.
+ROTATE_BYTES = 512 * 2 ** 20
+
+
+def _n_sets(k, v):
+    return max(1, math.ceil(ROTATE_BYTES / (k.numel() * k.element_size() + v.numel() * v.element_size())))
 
 
 def work(workload, L):
@@ -169,13 +180,22 @@ def run_sweep(torch, gqa_flash_attn, prefill_lens, decode_lens, dtype, gen):
         for L in lens:
             sq = L if workload == "prefill" else 1
             q, k, v = _make(torch, sq, L, dtype, gen)
-            k_sdpa, v_sdpa = _sdpa_expand(k, v)
-            ours_ms, mem = _time(torch, lambda: gqa_flash_attn(q, k, v, causal=True))
+            # decode: rotate K/V sets (and, for SDPA, expanded sets) past the
+            # Infinity Cache; prefill is MFMA-bound and uses one set
+            kvs = [(k, v)]
+            if workload == "decode":
+                kvs += [_make(torch, sq, L, dtype, gen)[1:] for _ in range(_n_sets(k, v) - 1)]
+            ours_ms, mem = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % len(kvs)], causal=True))
             try:
-                sdpa_ms = _time(torch, lambda: _sdpa_call(torch, q, k_sdpa, v_sdpa, sq == L))[0]
+                k_sdpa, v_sdpa = _sdpa_expand(k, v)
+                sdpa_kvs = [(k_sdpa, v_sdpa)]
+                if workload == "decode":
+                    sdpa_kvs += [_sdpa_expand(*kv) for kv in kvs[1:_n_sets(k_sdpa, v_sdpa)]]
+                sdpa_ms = _time(torch, lambda i: _sdpa_call(torch, q, *sdpa_kvs[i % len(sdpa_kvs)], sq == L))[0]
+                del k_sdpa, v_sdpa, sdpa_kvs
             except RuntimeError:
                 sdpa_ms = float("nan")
-            del k_sdpa, v_sdpa
+            del kvs
             row = make_row(workload, L, ours_ms, float("nan"), sdpa_ms, mem)
             rows.append(row)
             print(f"[{workload}] L={L:>5d}  ours={ours_ms:7.3f}ms  fa2=  n/a  ms  sdpa={sdpa_ms:7.3f}ms  "

@@ -246,12 +246,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // Six separate arrays (not one): the compiler can then tell the LDS-DMA
   // targets of later tiles from the buffers being read, and does not wait for
   // those loads before the reads.
-  __shared__ __attribute__((aligned(1024))) char sk0[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sk1[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sk2[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sv0[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sv1[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sv2[ST::kTileBytes];
+  // The V stages take the low 48 KiB: an MFMA phase reads V with twice as
+  // many LDS instructions as K, and below 64 KiB a stage's address fits the
+  // 16-bit offset field of ds_read, so those reads need no VALU address
+  // arithmetic (which would compete with the other wave's softmax on the
+  // SIMD).  The compiler lays kernel LDS variables out in name order.
+  __shared__ __attribute__((aligned(1024))) char lds0_v0[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds0_v1[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds0_v2[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds1_k0[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds1_k1[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds1_k2[ST::kTileBytes];
 
   const Dims& dm = p.dm;
   const int t = threadIdx.x, lane = t & 63;
@@ -430,11 +435,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
 
   auto kstage = [&](auto s3) -> char* {
     constexpr int S3 = decltype(s3)::value;
-    return S3 == 0 ? sk0 : (S3 == 1 ? sk1 : sk2);
+    return S3 == 0 ? lds1_k0 : (S3 == 1 ? lds1_k1 : lds1_k2);
   };
   auto vstage = [&](auto s3) -> char* {
     constexpr int S3 = decltype(s3)::value;
-    return S3 == 0 ? sv0 : (S3 == 1 ? sv1 : sv2);
+    return S3 == 0 ? lds0_v0 : (S3 == 1 ? lds0_v1 : lds0_v2);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -450,15 +455,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // Paged: the block(s) of the tile the next softmax phase issues.
   TileBlocks blk_next = tile_block(tb);
   if (grp == 0) {
-    issue_k(sk0, tb, blk_next);
+    issue_k(lds1_k0, tb, blk_next);
   } else {
-    issue_v(sv1, tb, blk_next);
+    issue_v(lds0_v1, tb, blk_next);
   }
   blk_next = tile_block(tb + 1);
   if (grp == 0) {
-    issue_k(sk1, tb + 1, blk_next);
+    issue_k(lds1_k1, tb + 1, blk_next);
   } else {
-    issue_v(sv2, tb + 1, blk_next);
+    issue_v(lds0_v2, tb + 1, blk_next);
   }
   blk_next = tile_block(tb + 2);
   u32x4 qreg[NKS];
@@ -704,7 +709,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     constexpr int CPR16 = 2 * D / 16;   // 16-byte chunks per row
     constexpr int RPI = 64 / CPR16;     // rows per store instruction
     const int sw = wave >> 1;
-    char* ot = (sw == 0 ? sk0 : sw == 1 ? sk1 : sw == 2 ? sk2 : sv0) + (wave & 1) * (32 * 2 * D);
+    char* ot = (sw == 0 ? lds1_k0 : sw == 1 ? lds1_k1 : sw == 2 ? lds1_k2 : lds0_v0) + (wave & 1) * (32 * 2 * D);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
