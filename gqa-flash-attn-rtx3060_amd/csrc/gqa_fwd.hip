@@ -413,6 +413,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
     ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
+  // K stages 1 and 2 lie above 64 KiB, out of reach of ds_read's 16-bit
+  // offset field.  Their reads address from kah = ka + the LDS address of
+  // stage 1, kept in registers (refreshed as opaque values in every MFMA
+  // phase, so the compiler neither folds them back into ka nor recomputes
+  // them): the stage and block offsets stay immediates, and the reads need
+  // no VALU address arithmetic beside the other wave's softmax.
+  const uint32_t k1base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds1_k1;
+  uint32_t kah[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) kah[ks] = ka[ks] + k1base;
   uint32_t vb[NDB];
   {
     const int q = lane >> 4, ii = lane & 15;                  // 16-lane group, lane in group
@@ -506,8 +516,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       }
     }
     if constexpr (DO_S) {
+      if constexpr (decltype(s3)::value == 0) {
 #pragma unroll
-      for (int j = 0; j < NS; ++j) opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + ka[j >> 1]);
+        for (int j = 0; j < NS; ++j) opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + ka[j >> 1]);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) asm volatile("" : "+v"(kah[ks]));
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+          opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + (kah[j >> 1] - k1base));
+      }
     }
     if constexpr (DO_PV) {
 #pragma unroll
