@@ -24,6 +24,7 @@ reference's torch oracle, the reference's only CPU path) on a bounded sample
 of the same prefill workload, on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only WORKLOAD]
+                       [--config NAME]
 """
 from __future__ import annotations
 
@@ -246,6 +247,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
+    ap.add_argument("--config", default=None,
+                    help="with --only configs: time only the BASELINE configs whose name starts with this")
     ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b", "configs"],
                     default=None,
                     help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
@@ -358,7 +361,7 @@ def main() -> int:
         result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup,
                                   only={"chunked": "chunked", "70b": "70B"}[args.only])
     elif args.only == "configs":
-        result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup)
+        result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup, only=args.config)
 
     if result["value"] is None and "decode" in result:
         d = result["decode"]

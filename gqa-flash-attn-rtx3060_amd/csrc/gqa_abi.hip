@@ -399,6 +399,8 @@ int fused_impl(const void* q, const int64_t q_stride[4], const void* k, const in
   if (workspace == nullptr || counters == nullptr) return GQA_E_NULL;
   if ((int64_t)std::min(32, (num_heads / num_kv_heads) * seq_q) * splits > gqa::kFusedMaxRowSplitsHost)
     return GQA_E_SPLITS;
+  // The combine reads the partial accumulators at 32-bit byte offsets.
+  if ((uint64_t)batch * num_heads * seq_q * splits * head_dim * 4u > 0xFFFFFFF0ull) return GQA_E_SPLITS;
   if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || (reinterpret_cast<uintptr_t>(counters) & 3u) != 0)
     return GQA_E_STRIDE;
   if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;

@@ -327,6 +327,11 @@ __device__ inline void store_coherent(float* p, float v) {
 __device__ inline float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Four consecutive floats at byte offset `off` of buffer `r`, read the same
+// way (a 16-byte buffer load with sc1 set: cache-policy bit 4 on gfx950).
+__device__ inline f32x4 load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+}
 
 // ---------------------------------------------------------------------------
 // Workgroup-id remap: hardware hands consecutive workgroup ids to the 8 XCDs

@@ -33,6 +33,7 @@
 // two tiles ahead (group A: K, group B: V) and waits for the ones issued one
 // softmax phase earlier, so a load has two phases to land and the ring never
 // overwrites a stage that is still read.
+#include <algorithm>
 #include <type_traits>
 
 #include "gqa_common.hpp"
@@ -228,6 +229,14 @@ __device__ __forceinline__ void mphase_pipe() {
 // instruction gets its own descriptor).
 // D = 64 keeps to 128 VGPRs (four waves per SIMD): two workgroups share a
 // compute unit, which outweighs the shorter LDS-read lookahead it needs.
+//
+// Contiguous K/V at D = 128 (one workgroup per compute unit) runs
+// persistent: p.n_wg workgroups each work through a list of items (below),
+// and an item's start overlaps the previous item's end: as soon as the
+// finished item's output has left the LDS stages, the workgroup issues the
+// next item's first K/V tiles and Q, and the output stores drain while
+// those loads are in flight.  The workgroup launch between items leaves the
+// critical path.
 template <int DT, int D, int PG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void gqa_fwd_kernel(
     FwdParams p) {
@@ -237,6 +246,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   constexpr int CPR = ST::CPR;
   constexpr bool PAGED = PG != 0;
   constexpr bool SMALL = PG == 2;
+  constexpr bool PERSIST = PG == 0 && D == 128;
   // Block ids a wave needs per tile: one, or (small pages) one per LDS-DMA
   // instruction it issues.
   struct TileBlocks { int id[SMALL ? ST::NI : 1]; };
@@ -257,6 +267,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   __shared__ __attribute__((aligned(1024))) char lds1_k0[ST::kTileBytes];
   __shared__ __attribute__((aligned(1024))) char lds1_k1[ST::kTileBytes];
   __shared__ __attribute__((aligned(1024))) char lds1_k2[ST::kTileBytes];
+  __shared__ int s_last;
 
   const Dims& dm = p.dm;
   const int t = threadIdx.x, lane = t & 63;
@@ -264,74 +275,104 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   const int grp = wave >> 2;                                     // 0: group A, 1: group B
   const int gw = wave & 3;                                       // wave index in its group
   const int i = lane & 31, hh = lane >> 5;
+  const bool varlen = p.q_len != nullptr;
 
-  // Work item: heavy (late) query blocks first under causal, and every XCD
+  // Work items: heavy (late) query blocks first under causal, and every XCD
   // gets a contiguous range of items (same kv head -> same L2).  With a key
   // split, the n_split heaviest blocks of each (b, kv head) come as two
   // items: first the upper halves of their key ranges, then (in the usual
   // order) the lower halves and the unsplit blocks.
   const int n_items = p.n_mblk + p.n_split;
   const int total = n_items * dm.Hkv * dm.B;
-  const int w = xcd_remap(blockIdx.x, total);
-  const int bh = w / n_items;
-  const int idx = w - bh * n_items;
-  int pid_m, part;  // part: -1 whole key range, 0 lower half, 1 upper half
-  if (idx < p.n_split) {
-    pid_m = p.n_mblk - 1 - idx;
-    part = 1;
-  } else {
-    const int mrank = idx - p.n_split;
-    pid_m = dm.causal ? (p.n_mblk - 1 - mrank) : mrank;
-    part = (pid_m >= p.n_mblk - p.n_split) ? 0 : -1;
-  }
-  const int b = bh / dm.Hkv, kvh = bh - b * dm.Hkv;
-  // Keys of this sequence (paged: its own length, clamped to [0, Skv]),
-  // and its query rows (variable lengths: q_len[b], tokens from q_start[b]).
-  const int skv = PAGED ? min(max(load_uniform(p.seq_lens + b), 0), dm.Skv) : dm.Skv;
-  const bool varlen = p.q_len != nullptr;
-  const int sq = varlen ? min(max(load_uniform(p.q_len + b), 0), dm.Sq) : dm.Sq;
-  const int64_t tok0 = varlen ? (int64_t)load_uniform(p.q_start + b) : 0;
-  if (pid_m * p.block_m >= sq) return;  // a block past this sequence's queries (variable lengths)
-  // Element offset of (query row pos, head h) in q / o.
-  auto row_off = [&](const TensorRef& t, int pos_, int h) -> int64_t {
-    return varlen ? (tok0 + pos_) * t.ss + (int64_t)h * t.sh : (int64_t)b * t.sb + (int64_t)h * t.sh + (int64_t)pos_ * t.ss;
+  // The k-th item of this workgroup (-1: none).  One item per workgroup
+  // (xcd_remap), or persistent: the workgroups of XCD x (hardware ids x,
+  // x + 8, ...) take the XCD's item range round by round in snake order
+  // (round j: slot c takes item j*S + c, or j*S + S-1-c in odd rounds), so
+  // the heavy-first order hands every slot a mix of heavy and light items.
+  const int n_wg = PERSIST ? p.n_wg : total;
+  auto item_at = [&](int k) -> int {
+    if (!PERSIST) return k == 0 ? xcd_remap(blockIdx.x, total) : -1;
+    const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int S = (n_wg - x + 7) >> 3;  // workgroups on XCD x
+    const int q = total >> 3, r = total & 7;
+    const int lo = x * q + min(x, r), n = q + (x < r ? 1 : 0);
+    const int j = k;
+    const int e = j * S + ((j & 1) ? S - 1 - slot : slot);
+    return e < n ? lo + e : -1;
   };
 
-  // This lane's query row.
-  const int r = wave * 32 + i;
-  const int g = r / p.block_m, ml = r - g * p.block_m;
-  const int pos = pid_m * p.block_m + ml;
-  const bool valid = (g < dm.G) && (pos < sq);
-  const int head = kvh * dm.G + (g < dm.G ? g : 0);
-  const int qpos = pos + (skv - sq);
-
-  // Key range of this workgroup.
-  const int pos_lo = pid_m * p.block_m;
-  const int pos_hi = min(pos_lo + p.block_m, sq) - 1;
-  int kv_end = skv;
-  if (dm.causal) kv_end = min(skv, pos_hi + (skv - sq) + 1);
-  kv_end = max(kv_end, 0);
-  const int ntiles_all = (kv_end + ST::kKeys - 1) / ST::kKeys;
-  // This item's tiles [tb, tb + ntiles).
-  const int tsplit = ntiles_all >> 1;
-  const int tb = (part == 1) ? tsplit : 0;
-  const int ntiles = (part == 0) ? tsplit : ntiles_all - tb;
-  const int qpos_lo = pos_lo + (skv - sq);
-
-  // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
-  // each ending at the last byte of row seq_kv - 1, and per-lane offsets.
-  // The host guarantees (seq_kv + 192) * row stride * 2 < 2^31, so every
-  // offset below (up to two tiles past the end) fits 32 bits.
+  // One work item's parameters.
+  struct Item {
+    int b, kvh, bh, pid_m, part;  // part: -1 whole key range, 0 lower half, 1 upper half
+    int skv, sq, tb, ntiles, qpos_lo;
+    int64_t tok0;
+    int pos, head, qpos;  // this lane's query row
+    bool valid;
+    const char* kbh;
+    const char* vbh;
+    __amdgpu_buffer_rsrc_t rk, rv;
+    const int* table_row;
+  };
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
-  const char* kbh = static_cast<const char*>(p.k.ptr) +
-                    2 * ((PAGED ? 0 : (int64_t)b * p.k.sb) + (int64_t)kvh * p.k.sh);
-  const char* vbh = static_cast<const char*>(p.v.ptr) +
-                    2 * ((PAGED ? 0 : (int64_t)b * p.v.sb) + (int64_t)kvh * p.v.sh);
-  // (An empty key range gets an empty descriptor: every load reads zero.)
-  const bool flat = !PAGED && dm.Skv > 0;
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbh, flat ? (uint32_t)(dm.Skv - 1) * kssb + 2 * D : 0u);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbh, flat ? (uint32_t)(dm.Skv - 1) * vssb + 2 * D : 0u);
-  const int* table_row = PAGED ? p.block_table + (int64_t)b * p.table_stride : nullptr;
+  auto decode = [&](int w) __attribute__((always_inline)) -> Item {
+    Item x;
+    x.bh = w / n_items;
+    const int idx = w - x.bh * n_items;
+    if (idx < p.n_split) {
+      x.pid_m = p.n_mblk - 1 - idx;
+      x.part = 1;
+    } else {
+      const int mrank = idx - p.n_split;
+      x.pid_m = dm.causal ? (p.n_mblk - 1 - mrank) : mrank;
+      x.part = (x.pid_m >= p.n_mblk - p.n_split) ? 0 : -1;
+    }
+    x.b = x.bh / dm.Hkv;
+    x.kvh = x.bh - x.b * dm.Hkv;
+    // Keys of this sequence (paged: its own length, clamped to [0, Skv]),
+    // and its query rows (variable lengths: q_len[b], tokens from q_start[b]).
+    x.skv = PAGED ? min(max(load_uniform(p.seq_lens + x.b), 0), dm.Skv) : dm.Skv;
+    x.sq = varlen ? min(max(load_uniform(p.q_len + x.b), 0), dm.Sq) : dm.Sq;
+    x.tok0 = varlen ? (int64_t)load_uniform(p.q_start + x.b) : 0;
+    // This lane's query row.
+    const int r = wave * 32 + i;
+    const int g = r / p.block_m, ml = r - g * p.block_m;
+    x.pos = x.pid_m * p.block_m + ml;
+    x.valid = (g < dm.G) && (x.pos < x.sq);
+    x.head = x.kvh * dm.G + (g < dm.G ? g : 0);
+    x.qpos = x.pos + (x.skv - x.sq);
+    // Key range of this item: tiles [tb, tb + ntiles).
+    const int pos_lo = x.pid_m * p.block_m;
+    const int pos_hi = min(pos_lo + p.block_m, x.sq) - 1;
+    int kv_end = x.skv;
+    if (dm.causal) kv_end = min(x.skv, pos_hi + (x.skv - x.sq) + 1);
+    kv_end = max(kv_end, 0);
+    const int ntiles_all = (kv_end + ST::kKeys - 1) / ST::kKeys;
+    const int tsplit = ntiles_all >> 1;
+    x.tb = (x.part == 1) ? tsplit : 0;
+    x.ntiles = (x.part == 0) ? tsplit : ntiles_all - x.tb;
+    x.qpos_lo = pos_lo + (x.skv - x.sq);
+    // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
+    // each ending at the last byte of row seq_kv - 1.  The host guarantees
+    // (seq_kv + 192) * row stride * 2 < 2^31, so every offset (up to two
+    // tiles past the end) fits 32 bits.  (An empty key range gets an empty
+    // descriptor: every load reads zero.)
+    x.kbh = static_cast<const char*>(p.k.ptr) + 2 * ((PAGED ? 0 : (int64_t)x.b * p.k.sb) + (int64_t)x.kvh * p.k.sh);
+    x.vbh = static_cast<const char*>(p.v.ptr) + 2 * ((PAGED ? 0 : (int64_t)x.b * p.v.sb) + (int64_t)x.kvh * p.v.sh);
+    const bool flat = !PAGED && dm.Skv > 0;
+    x.rk = make_rsrc(x.kbh, flat ? (uint32_t)(dm.Skv - 1) * kssb + 2 * D : 0u);
+    x.rv = make_rsrc(x.vbh, flat ? (uint32_t)(dm.Skv - 1) * vssb + 2 * D : 0u);
+    x.table_row = PAGED ? p.block_table + (int64_t)x.b * p.table_stride : nullptr;
+    return x;
+  };
+
+  int k_item = 0;
+  Item it = decode(item_at(0));
+  if (!PERSIST && it.pid_m * p.block_m >= it.sq) return;  // a block past this sequence's queries (variable lengths)
+  // Element offset of (query row pos, head h) in q / o.
+  auto row_off = [&](const Item& x, const TensorRef& tr, int pos_, int h) -> int64_t {
+    return varlen ? (x.tok0 + pos_) * tr.ss + (int64_t)h * tr.sh
+                  : (int64_t)x.b * tr.sb + (int64_t)h * tr.sh + (int64_t)pos_ * tr.ss;
+  };
 
   const int lrow = lane / CPR;
   const uint32_t koff =
@@ -348,22 +389,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // (read only for rows that start inside the sequence).  The softmax phases
   // use block ids read one phase ahead (blk_next), so the table reads'
   // latency is off the issue path.
-  auto tile_block = [&](int tile) -> TileBlocks {
+  auto tile_block = [&](const Item& x, int tile) -> TileBlocks {
     TileBlocks tbk;
     const int key0 = tile * ST::kKeys;
     if constexpr (SMALL) {
 #pragma unroll
       for (int j = 0; j < ST::NI; ++j) {
         const int key = key0 + (j * 4 + gw) * ST::RPI;  // first row of instruction j
-        tbk.id[j] = key < skv ? load_uniform(table_row + (key >> p.block_shift)) : 0;
+        tbk.id[j] = key < x.skv ? load_uniform(x.table_row + (key >> p.block_shift)) : 0;
       }
     } else {
-      tbk.id[0] = (PAGED && key0 < skv) ? load_uniform(table_row + (key0 >> p.block_shift)) : 0;
+      tbk.id[0] = (PAGED && key0 < x.skv) ? load_uniform(x.table_row + (key0 >> p.block_shift)) : 0;
     }
     return tbk;
   };
-  auto issue_tile = [&](char* lds, const char* head, __amdgpu_buffer_rsrc_t rsrc, uint32_t rowb, uint32_t off,
-                        int64_t blk_stride, int tile, const TileBlocks& blk) {
+  auto issue_tile = [&](const Item& x, char* lds, const char* head, __amdgpu_buffer_rsrc_t rsrc, uint32_t rowb,
+                        uint32_t off, int64_t blk_stride, int tile, const TileBlocks& blk) {
     const int key0 = tile * ST::kKeys;
     if constexpr (SMALL) {
       // Instruction j loads rows [key, key + RPI) of the tile, one run in
@@ -374,7 +415,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       for (int j = 0; j < ST::NI; ++j) {
         const int step = j * 4 + gw;
         const int key = key0 + step * ST::RPI;
-        const int rows = skv - key;
+        const int rows = x.skv - key;
         __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
         if (rows > 0) {
           const char* base = head + 2 * ((int64_t)blk.id[j] * blk_stride +
@@ -384,7 +425,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(lds + step * 1024), 16, off, 0, 0, 0);
       }
     } else if constexpr (PAGED) {
-      const int rows = skv - key0;
+      const int rows = x.skv - key0;
       __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
       if (rows > 0) {
         const char* base =
@@ -394,14 +435,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       issue_tile_dma<D>(lds, rt, 0u, rowb, off, gw);
     } else {
       (void)blk;
+      (void)head;
       issue_tile_dma<D>(lds, rsrc, (uint32_t)key0 * rowb, rowb, off, gw);
     }
   };
-  auto issue_k = [&](char* lds, int tile, const TileBlocks& blk) {
-    issue_tile(lds, kbh, rk, kssb, koff, p.k.sb, tile, blk);
+  auto issue_k = [&](const Item& x, char* lds, int tile, const TileBlocks& blk) {
+    issue_tile(x, lds, x.kbh, x.rk, kssb, koff, p.k.sb, tile, blk);
   };
-  auto issue_v = [&](char* lds, int tile, const TileBlocks& blk) {
-    issue_tile(lds, vbh, rv, vssb, voff, p.v.sb, tile, blk);
+  auto issue_v = [&](const Item& x, char* lds, int tile, const TileBlocks& blk) {
+    issue_tile(x, lds, x.vbh, x.rv, vssb, voff, p.v.sb, tile, blk);
   };
 
   // LDS side: per-lane read offsets (the 32-key block, chunk and row offsets
@@ -435,13 +477,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   }
 
   f32x16 acc[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+  float m_run, l_run;
   const float c = dm.c;
   f32x16 sc[2];    // S^T of the current tile (MFMA phase -> softmax phase)
   u32x4 pk[2][2];  // P^T operands (softmax phase -> next MFMA phase)
+  u32x4 qreg[NKS];
 
   auto kstage = [&](auto s3) -> char* {
     constexpr int S3 = decltype(s3)::value;
@@ -457,37 +497,38 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   using BT = std::true_type;
   using BF = std::false_type;
 
-  // Prologue: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1) of stage 2
-  // (tile indices relative to tb).  The tile loads go first: the Q loads
-  // behind them touch 32 rows per instruction and, issued first, held the
-  // tile loads back by ~2 us.  An invalid row loads row 0 of its sequence
-  // (always present here) and is zeroed.
-  // Paged: the block(s) of the tile the next softmax phase issues.
-  TileBlocks blk_next = tile_block(tb);
-  if (grp == 0) {
-    issue_k(lds1_k0, tb, blk_next);
-  } else {
-    issue_v(lds0_v1, tb, blk_next);
-  }
-  blk_next = tile_block(tb + 1);
-  if (grp == 0) {
-    issue_k(lds1_k1, tb + 1, blk_next);
-  } else {
-    issue_v(lds0_v2, tb + 1, blk_next);
-  }
-  blk_next = tile_block(tb + 2);
-  u32x4 qreg[NKS];
-  {
-    const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(p.q, valid ? pos : 0, head);
+  // Prologue loads of item x: stage 0 = K(0), stage 1 = K(1) + V(0), and V(1)
+  // of stage 2 (tile indices relative to tb), then Q.  The tile loads go
+  // first: the Q loads behind them touch 32 rows per instruction and, issued
+  // first, held the tile loads back by ~2 us.  An invalid row loads row 0 of
+  // its sequence (always present here) and is zeroed.  Paged: returns the
+  // block(s) of the tile the first softmax phase issues.
+  auto prologue_q = [&](const Item& x) __attribute__((always_inline)) {
+    const T* qrow = static_cast<const T*>(p.q.ptr) + row_off(x, p.q, x.valid ? x.pos : 0, x.head);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
-      qreg[ks] = valid ? x : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
+      qreg[ks] = x.valid ? v : u32x4{0u, 0u, 0u, 0u};
     }
-  }
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // these loads and Q
-  phase_barrier();
-  if (grp == 1) phase_barrier();  // group B runs one phase behind
+  };
+  auto prologue_kv = [&](const Item& x) __attribute__((always_inline)) -> TileBlocks {
+    TileBlocks bn = tile_block(x, x.tb);
+    if (grp == 0) {
+      issue_k(x, lds1_k0, x.tb, bn);
+    } else {
+      issue_v(x, lds0_v1, x.tb, bn);
+    }
+    bn = tile_block(x, x.tb + 1);
+    if (grp == 0) {
+      issue_k(x, lds1_k1, x.tb + 1, bn);
+    } else {
+      issue_v(x, lds0_v2, x.tb + 1, bn);
+    }
+    bn = tile_block(x, x.tb + 2);
+    return bn;
+  };
+  TileBlocks blk_next = prologue_kv(it);
+  prologue_q(it);
 
   // MFMA phase tt: P*V of tile tt-1 and S^T of tile tt, from stage tt (ring
   // slot tt % 3).
@@ -562,22 +603,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     __builtin_amdgcn_sched_barrier(0);
-    const int ta = tb + tt;  // absolute tile index
+    const int ta = it.tb + tt;  // absolute tile index
     if (grp == 0) {
-      issue_k(kstage(std::integral_constant<int, (S3 + 2) % 3>{}), ta + 2, blk_next);
+      issue_k(it, kstage(std::integral_constant<int, (S3 + 2) % 3>{}), ta + 2, blk_next);
     } else {
-      issue_v(vstage(s3), ta + 2, blk_next);
+      issue_v(it, vstage(s3), ta + 2, blk_next);
     }
-    blk_next = tile_block(ta + 3);
+    blk_next = tile_block(it, ta + 3);
     const int key0 = ta * ST::kKeys;
-    const bool need_mask = (key0 + ST::kKeys > skv) || (dm.causal && key0 + ST::kKeys - 1 > qpos_lo);
+    const bool need_mask = (key0 + ST::kKeys > it.skv) || (dm.causal && key0 + ST::kKeys - 1 > it.qpos_lo);
     if (need_mask) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = key0 + 32 * mb + key_of(v, hh);
-          const bool off = key >= skv || (dm.causal && key > qpos);
+          const bool off = key >= it.skv || (dm.causal && key > it.qpos);
           sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
     }
@@ -612,153 +653,203 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     phase_barrier();
   };
 
-  if (ntiles > 0) {
-    mphase(I0{}, BF{}, BT{}, 0);
-    vphase(I0{}, 0);
-    int tt = 1;
-    for (; tt + 3 <= ntiles; tt += 3) {
-      mphase(I1{}, BT{}, BT{}, tt);
-      vphase(I1{}, tt);
-      mphase(I2{}, BT{}, BT{}, tt + 1);
-      vphase(I2{}, tt + 1);
-      mphase(I0{}, BT{}, BT{}, tt + 2);
-      vphase(I0{}, tt + 2);
-    }
-    if (tt < ntiles) {
-      mphase(I1{}, BT{}, BT{}, tt);
-      vphase(I1{}, tt);
-      ++tt;
-      if (tt < ntiles) {
-        mphase(I2{}, BT{}, BT{}, tt);
-        vphase(I2{}, tt);
-        ++tt;
-      }
-    }
-    const int s3 = tt % 3;
-    if (s3 == 0) mphase(I0{}, BT{}, BF{}, tt);
-    else if (s3 == 1) mphase(I1{}, BT{}, BF{}, tt);
-    else mphase(I2{}, BT{}, BF{}, tt);
-  } else {
+  for (;;) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+    m_run = -__builtin_inff();
+    l_run = 0.f;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the prologue loads
     phase_barrier();
-  }
-  if (grp == 0) phase_barrier();  // both groups pass the same number of barriers
-  // No LDS-DMA load (of a tile past the end) may still be writing when the
-  // stages are reused for the output below, nor when the workgroup exits.
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  __syncthreads();
+    if (grp == 1) phase_barrier();  // group B runs one phase behind
 
-  // Split query block: publish this half's state (reference max, lane
-  // partial row sum, accumulators, lane-major so each lane of the other
-  // item reads back exactly its own row); the item that completes the
-  // block's counter merges the other half into its registers and writes o.
-  // The counter is read first: when the other half has already published
-  // (counter 1), this item is the last one and skips publishing its own.
-  // Otherwise it publishes, then counts itself in; whichever item's
-  // increment finds 1 merges.  Every increment follows its item's completed
-  // stores, so a counter of 1 means the other state is readable.
-  if (part >= 0) {
-    constexpr int PF_ = kFwdPartFloats(D);
-    constexpr int NA = NDB * 16;  // accumulators per lane
-    const int slot = bh * p.n_split + (p.n_mblk - 1 - pid_m);
-    float* mine = p.part_ws + ((int64_t)slot * 2 + part) * PF_;
-    const float* other = p.part_ws + ((int64_t)slot * 2 + (1 - part)) * PF_;
-    __shared__ int s_last;
-    if (t == 0) s_last = __hip_atomic_load(&p.part_cnt[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+    const int ntiles = it.ntiles;
+    if (ntiles > 0) {
+      mphase(I0{}, BF{}, BT{}, 0);
+      vphase(I0{}, 0);
+      int tt = 1;
+      for (; tt + 3 <= ntiles; tt += 3) {
+        mphase(I1{}, BT{}, BT{}, tt);
+        vphase(I1{}, tt);
+        mphase(I2{}, BT{}, BT{}, tt + 1);
+        vphase(I2{}, tt + 1);
+        mphase(I0{}, BT{}, BT{}, tt + 2);
+        vphase(I0{}, tt + 2);
+      }
+      if (tt < ntiles) {
+        mphase(I1{}, BT{}, BT{}, tt);
+        vphase(I1{}, tt);
+        ++tt;
+        if (tt < ntiles) {
+          mphase(I2{}, BT{}, BT{}, tt);
+          vphase(I2{}, tt);
+          ++tt;
+        }
+      }
+      const int s3 = tt % 3;
+      if (s3 == 0) mphase(I0{}, BT{}, BF{}, tt);
+      else if (s3 == 1) mphase(I1{}, BT{}, BF{}, tt);
+      else mphase(I2{}, BT{}, BF{}, tt);
+    } else {
+      phase_barrier();
+    }
+    if (grp == 0) phase_barrier();  // both groups pass the same number of barriers
+    // No LDS-DMA load (of a tile past the end) may still be writing when the
+    // stages are reused (by the next item, or for the output below), nor
+    // when the workgroup exits.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
-    if (!s_last) {
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t, acc[db][v]);
-      store_coherent(mine + NA * kFwdThreads + t, m_run);
-      store_coherent(mine + (NA + 1) * kFwdThreads + t, l_run);
-      __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
-      __syncthreads();
-      if (t == 0) s_last = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
-      __syncthreads();
-      if (!s_last) return;
-    }
-    // Both halves have arrived: leave the counter zero for the next call.
-    if (t == 0) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // The merge is written in terms of the lower (0) and upper (1) half, not
-    // of this item and the other one, so the rounding (fma contraction
-    // included) does not depend on which half finished last: repeated
-    // calls give identical outputs.
-    const bool lo = part == 0;
-    const float m_o = load_coherent(other + NA * kFwdThreads + t);
-    const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t);
-    const float m0 = lo ? m_run : m_o, m1 = lo ? m_o : m_run;
-    const float mm = fmaxf(m0, m1);
-    const float mu = (mm == -__builtin_inff()) ? 0.f : mm;
-    const float a0 = fast_exp2((m0 - mu) * c), a1 = fast_exp2((m1 - mu) * c);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float x_o = load_coherent(other + (db * 16 + v) * kFwdThreads + t);
-        const float x0 = lo ? acc[db][v] : x_o, x1 = lo ? x_o : acc[db][v];
-        acc[db][v] = __builtin_fmaf(x0, a0, x1 * a1);
-      }
-    const float l0 = lo ? l_run : l_o, l1 = lo ? l_o : l_run;
-    l_run = __builtin_fmaf(l0, a0, l1 * a1);
-    m_run = mm;
-  }
 
-  // Epilogue: o = acc / l (0/0 = NaN for a row whose keys are all masked, as
-  // the reference's acc / l_i at gqa_fwd.py:106).  A sequence with no keys
-  // at all gives zero rows instead: tests/reference.py:33-34 takes the
-  // softmax over an empty key axis and multiplies it with an empty V.
-  // Optional LSE side output: ln sum_k exp(s_k * D^-0.5) = (m_ref * c +
-  // log2 l) * ln 2 (l is relative to the reference point m_ref); -inf for a
-  // row with no visible key.
-  const float l_tot = xhalf_sum(l_run);
-  const float inv = skv == 0 ? 0.f : 1.0f / l_tot;
-  if (p.lse != nullptr && valid && hh == 0) {
-    // (B, Hq, Sq), or (tokens, Hq) with variable lengths.
-    const int64_t li = varlen ? (tok0 + pos) * dm.Hq + head : ((int64_t)b * dm.Hq + head) * dm.Sq + pos;
-    p.lse[li] = (m_run * c + __log2f(l_tot)) * kLn2;
-  }
-  // The wave's 32 x D output tile goes through LDS (row-major, 16-byte
-  // chunks XOR-swizzled by row; two waves per former K/V stage), so that it
-  // leaves as whole rows: each store instruction writes 64 lanes x 16 bytes
-  // covering RPI complete rows, where storing straight from the O^T
-  // accumulators would write 16 bytes into each of 32 rows per instruction.
-  {
-    constexpr int CPR16 = 2 * D / 16;   // 16-byte chunks per row
-    constexpr int RPI = 64 / CPR16;     // rows per store instruction
-    const int sw = wave >> 1;
-    char* ot = (sw == 0 ? lds1_k0 : sw == 1 ? lds1_k1 : sw == 2 ? lds1_k2 : lds0_v0) + (wave & 1) * (32 * 2 * D);
+    const int w_next = PERSIST ? item_at(k_item + 1) : -1;
+
+    // Split query block: publish this half's state (reference max, lane
+    // partial row sum, accumulators, lane-major so each lane of the other
+    // item reads back exactly its own row); the item that completes the
+    // block's counter merges the other half into its registers and writes o.
+    // The counter is read first: when the other half has already published
+    // (counter 1), this item is the last one and skips publishing its own.
+    // Otherwise it publishes, then counts itself in; whichever item's
+    // increment finds 1 merges.  Every increment follows its item's completed
+    // stores, so a counter of 1 means the other state is readable.
+    bool write_out = true;
+    if (it.part >= 0) {
+      constexpr int PF_ = kFwdPartFloats(D);
+      constexpr int NA = NDB * 16;  // accumulators per lane
+      const int slot = it.bh * p.n_split + (p.n_mblk - 1 - it.pid_m);
+      float* mine = p.part_ws + ((int64_t)slot * 2 + it.part) * PF_;
+      const float* other = p.part_ws + ((int64_t)slot * 2 + (1 - it.part)) * PF_;
+      if (t == 0) s_last = __hip_atomic_load(&p.part_cnt[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+      __syncthreads();
+      bool last = s_last;
+      if (!last) {
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x2 x;
-        x[0] = E::pack2(acc[db][4 * j] * inv, acc[db][4 * j + 1] * inv);
-        x[1] = E::pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv);
-        const int ch = (4 * db + j) ^ (i & (CPR16 - 1));
-        *reinterpret_cast<u32x2*>(ot + i * (2 * D) + ch * 16 + 8 * hh) = x;
+          for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t, acc[db][v]);
+        store_coherent(mine + NA * kFwdThreads + t, m_run);
+        store_coherent(mine + (NA + 1) * kFwdThreads + t, l_run);
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+        __syncthreads();
+        if (t == 0) s_last = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+        __syncthreads();
+        last = s_last;
       }
-    __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's LDS writes before its reads
-    const int c = lane % CPR16;
+      __syncthreads();  // every wave has read s_last before the next item's writes it
+      if (last) {
+        // Both halves have arrived: leave the counter zero for the next call.
+        if (t == 0) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // The merge is written in terms of the lower (0) and upper (1) half,
+        // not of this item and the other one, so the rounding (fma
+        // contraction included) does not depend on which half finished
+        // last: repeated calls give identical outputs.
+        const bool lo = it.part == 0;
+        const float m_o = load_coherent(other + NA * kFwdThreads + t);
+        const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t);
+        const float m0 = lo ? m_run : m_o, m1 = lo ? m_o : m_run;
+        const float mm = fmaxf(m0, m1);
+        const float mu = (mm == -__builtin_inff()) ? 0.f : mm;
+        const float a0 = fast_exp2((m0 - mu) * c), a1 = fast_exp2((m1 - mu) * c);
 #pragma unroll
-    for (int it = 0; it < 32 / RPI; ++it) {
-      const int rr = RPI * it + lane / CPR16;  // row of the tile
-      const u32x4 x = *reinterpret_cast<const u32x4*>(ot + rr * (2 * D) + ((c ^ (rr & (CPR16 - 1))) * 16));
-      const int r2 = wave * 32 + rr;
-      const int g2 = r2 / p.block_m, pos2 = pid_m * p.block_m + (r2 - g2 * p.block_m);
-      if (g2 < dm.G && pos2 < sq) {
-        T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(p.o, pos2, kvh * dm.G + g2);
-        *reinterpret_cast<u32x4*>(orow + 8 * c) = x;
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float x_o = load_coherent(other + (db * 16 + v) * kFwdThreads + t);
+            const float x0 = lo ? acc[db][v] : x_o, x1 = lo ? x_o : acc[db][v];
+            acc[db][v] = __builtin_fmaf(x0, a0, x1 * a1);
+          }
+        const float l0 = lo ? l_run : l_o, l1 = lo ? l_o : l_run;
+        l_run = __builtin_fmaf(l0, a0, l1 * a1);
+        m_run = mm;
+      }
+      write_out = last;
+    }
+
+    if (write_out) {
+      // Epilogue: o = acc / l (0/0 = NaN for a row whose keys are all
+      // masked, as the reference's acc / l_i at gqa_fwd.py:106).  A sequence
+      // with no keys at all gives zero rows instead: tests/reference.py:33-34
+      // takes the softmax over an empty key axis and multiplies it with an
+      // empty V.  Optional LSE side output: ln sum_k exp(s_k * D^-0.5) =
+      // (m_ref * c + log2 l) * ln 2 (l is relative to the reference point
+      // m_ref); -inf for a row with no visible key.
+      const float l_tot = xhalf_sum(l_run);
+      const float inv = it.skv == 0 ? 0.f : 1.0f / l_tot;
+      if (p.lse != nullptr && it.valid && hh == 0) {
+        // (B, Hq, Sq), or (tokens, Hq) with variable lengths.
+        const int64_t li = varlen ? (it.tok0 + it.pos) * dm.Hq + it.head
+                                  : ((int64_t)it.b * dm.Hq + it.head) * dm.Sq + it.pos;
+        p.lse[li] = (m_run * c + __log2f(l_tot)) * kLn2;
+      }
+      {
+        // The wave's 32 x D output tile goes through LDS (row-major, 16-byte
+        // chunks XOR-swizzled by row; two waves per former K/V stage), so that
+        // it leaves as whole rows: each store instruction writes 64 lanes x 16
+        // bytes covering RPI complete rows, where storing straight from the
+        // O^T accumulators would write 16 bytes into each of 32 rows per
+        // instruction.
+        constexpr int CPR16 = 2 * D / 16;  // 16-byte chunks per row
+        constexpr int RPI = 64 / CPR16;    // rows per store instruction
+        const int sw = wave >> 1;
+        char* ot = (sw == 0 ? lds1_k0 : sw == 1 ? lds1_k1 : sw == 2 ? lds1_k2 : lds0_v0) + (wave & 1) * (32 * 2 * D);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            u32x2 x;
+            x[0] = E::pack2(acc[db][4 * j] * inv, acc[db][4 * j + 1] * inv);
+            x[1] = E::pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv);
+            const int ch = (4 * db + j) ^ (i & (CPR16 - 1));
+            *reinterpret_cast<u32x2*>(ot + i * (2 * D) + ch * 16 + 8 * hh) = x;
+          }
+        __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's LDS writes before its reads
+        const int cc = lane % CPR16;
+#pragma unroll
+        for (int ri = 0; ri < 32 / RPI; ++ri) {
+          const int rr = RPI * ri + lane / CPR16;  // row of the tile
+          const u32x4 x = *reinterpret_cast<const u32x4*>(ot + rr * (2 * D) + ((cc ^ (rr & (CPR16 - 1))) * 16));
+          const int r2 = wave * 32 + rr;
+          const int g2 = r2 / p.block_m, pos2 = it.pid_m * p.block_m + (r2 - g2 * p.block_m);
+          if (g2 < dm.G && pos2 < it.sq) {
+            T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(it, p.o, pos2, it.kvh * dm.G + g2);
+            *reinterpret_cast<u32x4*>(orow + 8 * cc) = x;
+          }
+        }
       }
     }
+    if (!PERSIST || w_next < 0) break;
+    // Persistent: the next item's first tiles (once every wave's output has
+    // left the stages) and Q, loaded while the output stores drain.
+    __syncthreads();
+    it = decode(w_next);
+    blk_next = prologue_kv(it);
+    prologue_q(it);
+    ++k_item;
   }
 }
 
+// Compute units of the current device (one persistent workgroup each),
+// cached per device.
+static int device_cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
 template <int DT, int D, int PG>
-static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
+static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
   const int total = (p.n_mblk + p.n_split) * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(total), dim3(kFwdThreads), 0, stream, p);
+  int grid = total;
+  if (PG == 0 && D == 128) {
+    const int cus = device_cu_count();
+    grid = cus > 0 ? std::min(total, cus) : total;
+    p.n_wg = grid;
+  }
+  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -47,6 +47,9 @@ struct FwdParams {
   // and sequence b has q_len[b] <= Sq query rows.
   const int* q_start;
   const int* q_len;
+  // Persistent single pass (contiguous K/V, head_dim 128): workgroups
+  // launched, each working through a list of items (set by launch_fwd).
+  int n_wg;
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).

@@ -42,11 +42,15 @@ constexpr int kFusedMaxRowSplits = 4096;
 
 // Log-sum-exp combine of all splits for the R valid rows of one (b, kv head,
 // 32-row block), by one workgroup (gqa_split.py:134-147), spread over all 256
-// threads so the tail it adds stays short:
-//   1. m and l of every (row, split) into LDS; per-row m*; a = exp2(m - m*);
-//      l* = sum a * l;
-//   2. work items (split group, row, 4 columns): each sums a * acc over its
-//      splits; the split groups are then added up in LDS and o = sum / l*.
+// threads so the tail it adds stays short (every phase is one round of
+// loads in flight together, then LDS and wave reductions):
+//   1. m and l of every (row, split) into LDS; per row (one wave, lanes over
+//      the splits): m* (wave max), a = exp2(m - m*), l* = sum a * l (wave
+//      sum);
+//   2. work items (split group, row, 4 columns), one per thread where R * D
+//      / 4 <= 256: each sums a * acc over its splits with 16-byte
+//      device-coherent loads, 16 splits in flight; the split groups are then
+//      added up in LDS and o = sum / l*.
 // scratch: >= 2*R*S + 2*32 floats plus 1024 f32x4 (reuses the tile buffer).
 template <int DT, int D>
 __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb, int t, float* scratch) {
@@ -57,6 +61,7 @@ __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb
   const int S = p.splits;
   const int r0 = 32 * rb;
   const int R = min(32, dm.G * dm.Sq - r0);  // valid rows: position-major packing
+  const int lane = t & 63, wave = t >> 6;
   float* ma = scratch;              // [R][S]: m, then the scale factors a
   float* la = ma + R * S;           // [R][S]: l
   float* mst = la + R * S;          // [32]: m* per row
@@ -76,42 +81,48 @@ __device__ inline void combine_rows(const SplitParams& p, int b, int kvh, int rb
     la[f] = load_coherent(p.ws_l + ix);
   }
   __syncthreads();
-  if (t < R) {
+  for (int rl = wave; rl < R; rl += 4) {
     float m = -__builtin_inff();
-    for (int sp = 0; sp < S; ++sp) m = fmaxf(m, ma[t * S + sp]);
-    mst[t] = m;
-  }
-  __syncthreads();
-  // exp2(-inf - -inf) = NaN when every chunk of a row is empty, as the
-  // reference's combine (gqa_split.py:138) gives.
-  for (int f = t; f < R * S; f += 256) ma[f] = fast_exp2(ma[f] - mst[f / S]);
-  __syncthreads();
-  if (t < R) {
+    for (int sp = lane; sp < S; sp += 64) m = fmaxf(m, ma[rl * S + sp]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    // exp2(-inf - -inf) = NaN when every chunk of a row is empty, as the
+    // reference's combine (gqa_split.py:138) gives.
     float l = 0.f;
-    for (int sp = 0; sp < S; ++sp) l += ma[t * S + sp] * la[t * S + sp];
-    lst[t] = l;
-    // LSE of a row with no visible key is -inf (its o stays NaN).
-    if (p.lse != nullptr)
-      p.lse[row_index(t) / S] = mst[t] == -__builtin_inff() ? -__builtin_inff() : (mst[t] + __log2f(l)) * kLn2;
+    for (int sp = lane; sp < S; sp += 64) {
+      const float a = fast_exp2(ma[rl * S + sp] - m);
+      ma[rl * S + sp] = a;
+      l += a * la[rl * S + sp];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+    if (lane == 0) {
+      mst[rl] = m;
+      lst[rl] = l;
+      // LSE of a row with no visible key is -inf (its o stays NaN).
+      if (p.lse != nullptr)
+        p.lse[row_index(rl) / S] = m == -__builtin_inff() ? -__builtin_inff() : (m + __log2f(l)) * kLn2;
+    }
   }
+  __syncthreads();
 
-  // Split groups: enough work items (<= 1024) to keep many loads in flight.
-  int nsg = 1024 / (R * NDP);
+  // Split groups: one work item per thread (or as many as R * D / 4 needs),
+  // each with a long run of independent loads.
+  int nsg = 256 / (R * NDP);
   nsg = max(1, min(nsg, S));
   const int items = nsg * R * NDP;
+  // 16-byte loads through a buffer descriptor over the whole acc workspace
+  // (its size fits the 32-bit offsets: the launcher bounds it).
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
   for (int it = t; it < items; it += 256) {
     const int d4 = it % NDP;
     const int rl = (it / NDP) % R;
     const int sg = it / (NDP * R);
-    const float* wa = p.ws_acc + row_index(rl) * D + 4 * d4;
+    const uint32_t base = (uint32_t)(row_index(rl) * D + 4 * d4) * 4u;
     const float* a = ma + rl * S;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int sp = sg; sp < S; sp += nsg) {
-      const float* src = wa + (int64_t)sp * D;
-      const f32x4 x = {load_coherent(src), load_coherent(src + 1), load_coherent(src + 2), load_coherent(src + 3)};
-      o += a[sp] * x;
-    }
+#pragma unroll 16
+    for (int sp = sg; sp < S; sp += nsg) o += a[sp] * load_coherent4(ra, base + (uint32_t)sp * (D * 4));
     red[it] = o;
   }
   __syncthreads();

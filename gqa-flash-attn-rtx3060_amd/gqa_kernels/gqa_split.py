@@ -81,6 +81,8 @@ LOG2E = math.log2(math.e)
 # The fused combine stages (valid rows of a 32-row block) x splits values in
 # LDS; above this bound the two-launch form is used.
 FUSED_MAX_ROW_SPLITS = 4096
+# ... and addresses the partial accumulators with 32-bit byte offsets.
+FUSED_MAX_ACC_BYTES = 0xFFFFFFF0
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 
@@ -120,7 +122,8 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False, retur
     lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
 
     group = num_heads // num_kv_heads
-    if fused and min(32, group * seq_q) * splits <= FUSED_MAX_ROW_SPLITS:
+    if (fused and min(32, group * seq_q) * splits <= FUSED_MAX_ROW_SPLITS
+            and batch * num_heads * seq_q * splits * head_dim * 4 <= FUSED_MAX_ACC_BYTES):
         n = lib.gqa_split_counters_count(batch, num_heads, num_kv_heads, seq_q)
         counters = _counter_buffer(q.device, stream, n)
         qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),

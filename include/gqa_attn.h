@@ -173,8 +173,11 @@ size_t gqa_split_counters_count(int batch, int num_heads, int num_kv_heads, int 
  * counters (gqa_split_counters_count ints) must be zero on entry; the kernel
  * leaves them zero, so one counter buffer can serve every call made on one
  * stream (calls that overlap in time need separate buffers).  The combine
- * stages min(32, G*seq_q) * splits values in LDS: above 4096 this returns
- * GQA_E_SPLITS (use gqa_split_first_launch + gqa_split_reduce_launch). */
+ * stages min(32, G*seq_q) * splits values in LDS and addresses the fp32
+ * partials with 32-bit offsets: above 4096 values, or with more than
+ * 2^32 - 16 bytes of partial accumulators (batch * num_heads * seq_q *
+ * splits * head_dim * 4), this returns GQA_E_SPLITS (use
+ * gqa_split_first_launch + gqa_split_reduce_launch). */
 int gqa_split_fused_launch(const void* q, const int64_t q_stride[4],
                            const void* k, const int64_t k_stride[4],
                            const void* v, const int64_t v_stride[4],
