@@ -252,7 +252,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   struct TileBlocks { int id[SMALL ? ST::NI : 1]; };
   constexpr int NDB = D / 32;  // 32-wide d blocks of O^T
   constexpr int NKS = D / 16;  // k-steps of S^T
-  constexpr int PF = (D == 64) ? 4 : 6;  // MFMA slots of LDS-read lookahead
+  constexpr int PF = (D == 64) ? 3 : 6;  // MFMA slots of LDS-read lookahead
   // Six separate arrays (not one): the compiler can then tell the LDS-DMA
   // targets of later tiles from the buffers being read, and does not wait for
   // those loads before the reads.
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     const int* table_row;
   };
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
-  auto decode = [&](int w) __attribute__((always_inline)) -> Item {
+  auto decode = [&](int w, int i, int block_m) __attribute__((always_inline)) -> Item {
     Item x;
     x.bh = w / n_items;
     const int idx = w - x.bh * n_items;
@@ -335,14 +335,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     x.tok0 = varlen ? (int64_t)load_uniform(p.q_start + x.b) : 0;
     // This lane's query row.
     const int r = wave * 32 + i;
-    const int g = r / p.block_m, ml = r - g * p.block_m;
-    x.pos = x.pid_m * p.block_m + ml;
+    const int g = r / block_m, ml = r - g * block_m;
+    x.pos = x.pid_m * block_m + ml;
     x.valid = (g < dm.G) && (x.pos < x.sq);
     x.head = x.kvh * dm.G + (g < dm.G ? g : 0);
     x.qpos = x.pos + (x.skv - x.sq);
     // Key range of this item: tiles [tb, tb + ntiles).
-    const int pos_lo = x.pid_m * p.block_m;
-    const int pos_hi = min(pos_lo + p.block_m, x.sq) - 1;
+    const int pos_lo = x.pid_m * block_m;
+    const int pos_hi = min(pos_lo + block_m, x.sq) - 1;
     int kv_end = x.skv;
     if (dm.causal) kv_end = min(x.skv, pos_hi + (x.skv - x.sq) + 1);
     kv_end = max(kv_end, 0);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   };
 
   int k_item = 0;
-  Item it = decode(item_at(0));
+  Item it = decode(item_at(0), i, p.block_m);
   if (!PERSIST && it.pid_m * p.block_m >= it.sq) return;  // a block past this sequence's queries (variable lengths)
   // Element offset of (query row pos, head h) in q / o.
   auto row_off = [&](const Item& x, const TensorRef& tr, int pos_, int h) -> int64_t {
@@ -455,16 +455,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
     ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
-  // K stages 1 and 2 lie above 64 KiB, out of reach of ds_read's 16-bit
-  // offset field.  Their reads address from kah = ka + the LDS address of
-  // stage 1, kept in registers (refreshed as opaque values in every MFMA
-  // phase, so the compiler neither folds them back into ka nor recomputes
-  // them): the stage and block offsets stay immediates, and the reads need
-  // no VALU address arithmetic beside the other wave's softmax.
+  // At D = 128, K stages 1 and 2 lie above 64 KiB, out of reach of
+  // ds_read's 16-bit offset field.  Their reads address from kah = ka + the
+  // LDS address of stage 1, kept in registers (refreshed as opaque values in
+  // every MFMA phase, so the compiler neither folds them back into ka nor
+  // recomputes them): the stage and block offsets stay immediates, and the
+  // reads need no VALU address arithmetic beside the other wave's softmax.
+  // (At D = 64 every stage lies below 64 KiB.)
+  constexpr bool kHighK = 6 * ST::kTileBytes > 65536;
   const uint32_t k1base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds1_k1;
-  uint32_t kah[NKS];
+  uint32_t kah[kHighK ? NKS : 1];
 #pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) kah[ks] = ka[ks] + k1base;
+  for (int ks = 0; ks < (kHighK ? NKS : 1); ++ks) kah[ks] = ka[ks] + k1base;
   uint32_t vb[NDB];
   {
     const int q = lane >> 4, ii = lane & 15;                  // 16-lane group, lane in group
@@ -557,7 +559,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       }
     }
     if constexpr (DO_S) {
-      if constexpr (decltype(s3)::value == 0) {
+      if constexpr (decltype(s3)::value == 0 || !kHighK) {
 #pragma unroll
         for (int j = 0; j < NS; ++j) opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + ka[j >> 1]);
       } else {
@@ -700,6 +702,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     __syncthreads();
 
     const int w_next = PERSIST ? item_at(k_item + 1) : -1;
+    // This item's parameters and the lane ids again, from the item index,
+    // block_m and a zero laundered through SGPRs (the lane id through
+    // v_mbcnt): kept from the start, the values read only here would stay
+    // live across the whole tile loop (at D = 64, in scratch).
+    int w_cur = item_at(k_item), zero = 0, bm = p.block_m;
+    asm volatile("" : "+s"(w_cur), "+s"(zero), "+s"(bm));
+    const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, (unsigned)zero));
+    const int t_e = wave * 64 + lane_e, i_e = lane_e & 31, hh_e = lane_e >> 5;
+    const Item ie = decode(w_cur, i_e, bm);
 
     // Split query block: publish this half's state (reference max, lane
     // partial row sum, accumulators, lane-major so each lane of the other
@@ -711,39 +722,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     // increment finds 1 merges.  Every increment follows its item's completed
     // stores, so a counter of 1 means the other state is readable.
     bool write_out = true;
-    if (it.part >= 0) {
+    if (ie.part >= 0) {
       constexpr int PF_ = kFwdPartFloats(D);
       constexpr int NA = NDB * 16;  // accumulators per lane
-      const int slot = it.bh * p.n_split + (p.n_mblk - 1 - it.pid_m);
-      float* mine = p.part_ws + ((int64_t)slot * 2 + it.part) * PF_;
-      const float* other = p.part_ws + ((int64_t)slot * 2 + (1 - it.part)) * PF_;
-      if (t == 0) s_last = __hip_atomic_load(&p.part_cnt[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+      const int slot = ie.bh * p.n_split + (p.n_mblk - 1 - ie.pid_m);
+      float* mine = p.part_ws + ((int64_t)slot * 2 + ie.part) * PF_;
+      const float* other = p.part_ws + ((int64_t)slot * 2 + (1 - ie.part)) * PF_;
+      if (t_e == 0) s_last = __hip_atomic_load(&p.part_cnt[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
       __syncthreads();
       bool last = s_last;
       if (!last) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t, acc[db][v]);
-        store_coherent(mine + NA * kFwdThreads + t, m_run);
-        store_coherent(mine + (NA + 1) * kFwdThreads + t, l_run);
+          for (int v = 0; v < 16; ++v) store_coherent(mine + (db * 16 + v) * kFwdThreads + t_e, acc[db][v]);
+        store_coherent(mine + NA * kFwdThreads + t_e, m_run);
+        store_coherent(mine + (NA + 1) * kFwdThreads + t_e, l_run);
         __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
         __syncthreads();
-        if (t == 0) s_last = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+        if (t_e == 0) s_last = __hip_atomic_fetch_add(&p.part_cnt[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
         __syncthreads();
         last = s_last;
       }
       __syncthreads();  // every wave has read s_last before the next item's writes it
       if (last) {
         // Both halves have arrived: leave the counter zero for the next call.
-        if (t == 0) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t_e == 0) __hip_atomic_store(&p.part_cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // The merge is written in terms of the lower (0) and upper (1) half,
         // not of this item and the other one, so the rounding (fma
         // contraction included) does not depend on which half finished
         // last: repeated calls give identical outputs.
-        const bool lo = it.part == 0;
-        const float m_o = load_coherent(other + NA * kFwdThreads + t);
-        const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t);
+        const bool lo = ie.part == 0;
+        const float m_o = load_coherent(other + NA * kFwdThreads + t_e);
+        const float l_o = load_coherent(other + (NA + 1) * kFwdThreads + t_e);
         const float m0 = lo ? m_run : m_o, m1 = lo ? m_o : m_run;
         const float mm = fmaxf(m0, m1);
         const float mu = (mm == -__builtin_inff()) ? 0.f : mm;
@@ -752,7 +763,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const float x_o = load_coherent(other + (db * 16 + v) * kFwdThreads + t);
+            const float x_o = load_coherent(other + (db * 16 + v) * kFwdThreads + t_e);
             const float x0 = lo ? acc[db][v] : x_o, x1 = lo ? x_o : acc[db][v];
             acc[db][v] = __builtin_fmaf(x0, a0, x1 * a1);
           }
@@ -772,11 +783,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       // (m_ref * c + log2 l) * ln 2 (l is relative to the reference point
       // m_ref); -inf for a row with no visible key.
       const float l_tot = xhalf_sum(l_run);
-      const float inv = it.skv == 0 ? 0.f : 1.0f / l_tot;
-      if (p.lse != nullptr && it.valid && hh == 0) {
+      const float inv = ie.skv == 0 ? 0.f : 1.0f / l_tot;
+      if (p.lse != nullptr && ie.valid && hh_e == 0) {
         // (B, Hq, Sq), or (tokens, Hq) with variable lengths.
-        const int64_t li = varlen ? (it.tok0 + it.pos) * dm.Hq + it.head
-                                  : ((int64_t)it.b * dm.Hq + it.head) * dm.Sq + it.pos;
+        const int64_t li = varlen ? (ie.tok0 + ie.pos) * dm.Hq + ie.head
+                                  : ((int64_t)ie.b * dm.Hq + ie.head) * dm.Sq + ie.pos;
         p.lse[li] = (m_run * c + __log2f(l_tot)) * kLn2;
       }
       {
@@ -797,19 +808,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
             u32x2 x;
             x[0] = E::pack2(acc[db][4 * j] * inv, acc[db][4 * j + 1] * inv);
             x[1] = E::pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv);
-            const int ch = (4 * db + j) ^ (i & (CPR16 - 1));
-            *reinterpret_cast<u32x2*>(ot + i * (2 * D) + ch * 16 + 8 * hh) = x;
+            const int ch = (4 * db + j) ^ (i_e & (CPR16 - 1));
+            *reinterpret_cast<u32x2*>(ot + i_e * (2 * D) + ch * 16 + 8 * hh_e) = x;
           }
         __builtin_amdgcn_s_waitcnt(kLgkm0);  // this wave's LDS writes before its reads
-        const int cc = lane % CPR16;
+        const int cc = lane_e % CPR16;
 #pragma unroll
         for (int ri = 0; ri < 32 / RPI; ++ri) {
-          const int rr = RPI * ri + lane / CPR16;  // row of the tile
+          const int rr = RPI * ri + lane_e / CPR16;  // row of the tile
           const u32x4 x = *reinterpret_cast<const u32x4*>(ot + rr * (2 * D) + ((cc ^ (rr & (CPR16 - 1))) * 16));
           const int r2 = wave * 32 + rr;
-          const int g2 = r2 / p.block_m, pos2 = it.pid_m * p.block_m + (r2 - g2 * p.block_m);
-          if (g2 < dm.G && pos2 < it.sq) {
-            T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(it, p.o, pos2, it.kvh * dm.G + g2);
+          const int g2 = r2 / bm, pos2 = ie.pid_m * bm + (r2 - g2 * bm);
+          if (g2 < dm.G && pos2 < ie.sq) {
+            T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + row_off(ie, p.o, pos2, ie.kvh * dm.G + g2);
             *reinterpret_cast<u32x4*>(orow + 8 * cc) = x;
           }
         }
@@ -819,7 +830,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     // Persistent: the next item's first tiles (once every wave's output has
     // left the stages) and Q, loaded while the output stores drain.
     __syncthreads();
-    it = decode(w_next);
+    it = decode(w_next, i, p.block_m);
     blk_next = prologue_kv(it);
     prologue_q(it);
     ++k_item;
