@@ -431,14 +431,17 @@ def paged_prefill(torch, steps, warmup):
 
 
 # Every BASELINE config (BASELINE.json "configs"): name, B, Hq, Hkv, seq_q,
-# seq_kv and the roofline that bounds it.  configs[0] is the reference's CPU
-# config (decode at 2048 keys), here timed on the GPU beside its CPU time.
+# seq_kv, the roofline that bounds it and head_dim.  configs[0] is the
+# reference's CPU config (decode at 2048 keys), here timed on the GPU beside
+# its CPU time.  The last row is the 16K prefill at head_dim 64, the other
+# head size the reference accepts (dispatch.py:32).
 CONFIGS = (
-    [("cpu-config decode 2048", 1, 32, 8, 1, 2048, "hbm")]
-    + [(f"prefill {s}", 1, 32, 8, s, s, "mfma") for s in (2048, 4096, 8192, 16384)]
-    + [(f"decode {s}", 1, 32, 8, 1, s, "hbm") for s in (8192, 32768, 131072)]
-    + [("chunked prefill B=4 512/8192", 4, 32, 8, 512, 8192, "mfma"),
-       ("70B decode B=16 Hq=64 Sq=4 32768", 16, 64, 8, 4, 32768, "hbm")]
+    [("cpu-config decode 2048", 1, 32, 8, 1, 2048, "hbm", 128)]
+    + [(f"prefill {s}", 1, 32, 8, s, s, "mfma", 128) for s in (2048, 4096, 8192, 16384)]
+    + [(f"decode {s}", 1, 32, 8, 1, s, "hbm", 128) for s in (8192, 32768, 131072)]
+    + [("chunked prefill B=4 512/8192", 4, 32, 8, 512, 8192, "mfma", 128),
+       ("70B decode B=16 Hq=64 Sq=4 32768", 16, 64, 8, 4, 32768, "hbm", 128),
+       ("prefill 16384 head_dim 64", 1, 32, 8, 16384, 16384, "mfma", 64)]
 )
 # K/V sets rotated per HBM-bound config: enough that consecutive calls cannot
 # find the previous calls' keys in the 256 MB Infinity Cache.
@@ -446,27 +449,28 @@ ROTATE_BYTES = 600e6
 
 
 def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None):
-    """Time every BASELINE config (or the ones whose name starts with
-    `only`): mean µs over `steps` back-to-back calls (5x as many for
+    """Time every BASELINE config (or the one named `only`, else the ones
+    whose name starts with it): mean µs over `steps` back-to-back calls (5x as many for
     HBM-bound configs, which take microseconds) after `warmup` calls, with
     TFLOP/s, HBM GB/s and the fraction of the roofline that bounds the
     config.  HBM-bound configs rotate K/V sets (ROTATE_BYTES in total)."""
     from gqa_kernels.dispatch import _cu_count, choose_route
     rows = []
-    for name, b, hq, hkv, sq, skv, bound in CONFIGS:
-        if only is not None and not name.startswith(only):
-            continue
-        by1 = hbm_bytes(b, hq, hkv, sq, skv, D)
+    sel = CONFIGS
+    if only is not None:  # the config of that exact name, else those starting with it
+        sel = [c for c in CONFIGS if c[0] == only] or [c for c in CONFIGS if c[0].startswith(only)]
+    for name, b, hq, hkv, sq, skv, bound, d in sel:
+        by1 = hbm_bytes(b, hq, hkv, sq, skv, d)
         nset = max(1, math.ceil(ROTATE_BYTES / by1)) if bound == "hbm" else 1
-        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, D, seed=len(rows) + 11, n_kv_sets=nset)
+        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, d, seed=len(rows) + 11, n_kv_sets=nset)
         n = steps * 5 if bound == "hbm" else steps
         ms = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % nset], causal=True), n, warmup)
-        fl = flops(b, hq, sq, skv, D)
+        fl = flops(b, hq, sq, skv, d)
         tflops, gbs = fl / (ms * 1e-3) / 1e12, by1 / (ms * 1e-3) / 1e9
         achieved, peak, unit = (tflops, PEAK_BF16_TFLOPS, "TFLOP/s") if bound == "mfma" else \
             (gbs, PEAK_HBM_GBS, "GB/s")
         route = choose_route(b, hq, hkv, sq, skv, _cu_count(0))
-        rows.append({"config": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv, "D": D,
+        rows.append({"config": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv, "D": d,
                      "us": ms * 1e3, "tflops": tflops, "gbs": gbs, "steps": n, "kv_sets": nset,
                      "route": route.kind + (f" splits={route.splits}" if route.kind == "split" else
                                             f" key-split blocks={route.fwd_split}" if route.fwd_split else ""),
