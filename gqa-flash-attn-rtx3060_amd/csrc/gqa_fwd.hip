@@ -702,15 +702,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     __syncthreads();
 
     const int w_next = PERSIST ? item_at(k_item + 1) : -1;
-    // This item's parameters and the lane ids again, from the item index,
-    // block_m and a zero laundered through SGPRs (the lane id through
-    // v_mbcnt): kept from the start, the values read only here would stay
-    // live across the whole tile loop (at D = 64, in scratch).
+    // One workgroup per item: this item's parameters and the lane ids again,
+    // from the item index, block_m and a zero laundered through SGPRs (the
+    // lane id through v_mbcnt): kept from the start, the values read only
+    // here would stay live across the whole tile loop (at D = 64, in
+    // scratch).  The persistent kernel keeps them (and measured 35-60 %
+    // slower on short key-split prefills when re-deriving them).
     int w_cur = item_at(k_item), zero = 0, bm = p.block_m;
-    asm volatile("" : "+s"(w_cur), "+s"(zero), "+s"(bm));
-    const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, (unsigned)zero));
+    if constexpr (!PERSIST) asm volatile("" : "+s"(w_cur), "+s"(zero), "+s"(bm));
+    const int lane_e =
+        PERSIST ? lane : (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, (unsigned)zero));
     const int t_e = wave * 64 + lane_e, i_e = lane_e & 31, hh_e = lane_e >> 5;
-    const Item ie = decode(w_cur, i_e, bm);
+    const Item ie = PERSIST ? it : decode(w_cur, i_e, bm);
 
     // Split query block: publish this half's state (reference max, lane
     // partial row sum, accumulators, lane-major so each lane of the other
