@@ -21,7 +21,8 @@ using gqa::TensorRef;
 // 7: gqa_paged_split_first_launch limits a chunk over pages of < 64 keys to
 // GQA_PAGED_CHUNK_PAGES pages (GQA_E_SPLITS beyond); a sequence without keys
 // gives zero rows on every path.  8: gqa_split_noalloc_launch.
-constexpr int kAbiVersion = 8;
+// 9: gqa_split_launch (first pass and combine in one call).
+constexpr int kAbiVersion = 9;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -452,6 +453,24 @@ int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4], const v
   if (rc && batch > 0 && seq_q > 0) return rc;
   return fused_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, workspace, counters, splits, batch,
                     num_heads, num_kv_heads, seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
+}
+
+int gqa_split_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                     const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse,
+                     float* workspace, int splits, int batch, int num_heads, int num_kv_heads, int seq_q,
+                     int seq_kv, int head_dim, float scale_log2, int causal, int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
+  if (rc) return rc;
+  if (splits < 1 || splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  // o is checked before the first pass is enqueued (q, k, v and the
+  // workspace by the first pass).
+  if ((rc = check_tensor(o, o_stride))) return rc;
+  rc = gqa_split_first_launch(q, q_stride, k, k_stride, v, v_stride, workspace, splits, batch, num_heads,
+                              num_kv_heads, seq_q, seq_kv, head_dim, scale_log2, causal, dtype, stream);
+  if (rc) return rc;
+  return reduce_impl(workspace, splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream);
 }
 
 int gqa_split_reduce_launch(const float* workspace, int splits, void* o, const int64_t o_stride[4], int batch,

@@ -136,20 +136,17 @@ def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False, retur
             return o
         _lib.check(lib.gqa_split_fused_lse_launch(*qkvo, lse.data_ptr(), *rest))
         return o, lse
+    # First pass and combine through one C call (gqa_split_launch: the two
+    # launches of gqa_split.py:168-193, one ctypes transition).
     _lib.check(
-        lib.gqa_split_first_launch(
+        lib.gqa_split_launch(
             q.data_ptr(), _lib.strides(q),
             k.data_ptr(), _lib.strides(k),
             v.data_ptr(), _lib.strides(v),
+            o.data_ptr(), _lib.strides(o), None if lse is None else lse.data_ptr(),
             workspace.data_ptr(), splits,
             batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim,
             scale_log2, int(bool(causal)), dtype, stream,
         )
     )
-    if lse is None:
-        _lib.check(lib.gqa_split_reduce_launch(workspace.data_ptr(), splits, o.data_ptr(), _lib.strides(o),
-                                               batch, num_heads, seq_q, head_dim, dtype, stream))
-        return o
-    _lib.check(lib.gqa_split_reduce_lse_launch(workspace.data_ptr(), splits, o.data_ptr(), _lib.strides(o),
-                                               lse.data_ptr(), batch, num_heads, seq_q, head_dim, dtype, stream))
-    return o, lse
+    return o if lse is None else (o, lse)

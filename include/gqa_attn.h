@@ -199,6 +199,22 @@ int gqa_split_fused_lse_launch(const void* q, const int64_t q_stride[4],
                                float scale_log2, int causal, int dtype,
                                void* stream);
 
+/* The whole split-KV forward in one call: gqa_split_first_launch into
+ * `workspace`, then gqa_split_reduce_launch into o (gqa_split_reduce_lse_launch
+ * when lse is not NULL), both on `stream` — what reference
+ * gqa_kernels/gqa_split.py:153-194 (split_kv_forward) launches, with one
+ * host-to-library transition instead of two.  Arguments and errors as those
+ * two entry points; o (and lse) are checked before the first pass is
+ * enqueued. */
+int gqa_split_launch(const void* q, const int64_t q_stride[4],
+                     const void* k, const int64_t k_stride[4],
+                     const void* v, const int64_t v_stride[4],
+                     void* o, const int64_t o_stride[4], float* lse,
+                     float* workspace, int splits,
+                     int batch, int num_heads, int num_kv_heads,
+                     int seq_q, int seq_kv, int head_dim,
+                     float scale_log2, int causal, int dtype, void* stream);
+
 /* Split-KV forward that allocates nothing.  No counterpart in the reference:
  * it is for callers that cannot allocate device memory or hand in a
  * workspace (code under HIP graph capture, tight serving loops, harnesses
