@@ -1,0 +1,525 @@
+// gqa_decode.hip — split-KV first pass for short query blocks (decode) at
+// head_dim 128 over contiguous K/V, with an optional fused combine.
+//
+// Replaces, for these shapes, the Triton gqa_split_first_kernel (reference
+// gqa_kernels/gqa_split.py:26-112) and, when fused, gqa_split_reduce_kernel
+// (gqa_split.py:115-147).  The work decomposition, the packed rows and the
+// partials are those of gqa_split.hip: one workgroup per (batch, kv head,
+// 32-row block, split), rows packed position-major (row r -> position r / G,
+// head r % G), partials (m in log2 units, l, unnormalised acc) per (row,
+// split) in the same workspace layout.
+//
+// Streaming: the chunk's keys arrive in 64-key K and V tiles written
+// straight into LDS by buffer loads in their LDS-DMA form (no staging
+// registers, no VALU transposes), through a ring of two stages; a stage is
+// refilled with the tile two ahead as soon as every wave has read it, so one
+// to two tiles stay in flight per workgroup (two workgroups per CU).  V is
+// read transposed by ds_read_b64_tr_b16 (the single-pass kernel's layout,
+// gqa_lds.hpp).
+//
+// The 4 waves split the head dimension, not the keys: every wave computes
+// S^T = K Q^T for all 64 keys of a tile and the same exact online softmax
+// (the same instructions on the same data: bit-identical statistics in every
+// wave), and wave w accumulates O^T for dims [32w, 32w + 32).  At the end of
+// the chunk each wave stores its own 32 dims of the valid rows' partials —
+// no cross-wave merge.  With a decode group of 4 query rows most of each
+// S^T MFMA is padding; it runs hidden under the HBM stream.
+//
+// Fused combine (SplitParams::counters set): the last workgroup of each
+// (b, kv head, row block) to count its partial in combines all splits
+// (gqa_split.py:134-147) with one round of global loads — m and l of every
+// (row, split) and this thread's accumulators are requested together.
+#include <type_traits>
+
+#include "gqa_common.hpp"
+#include "gqa_lds.hpp"
+#include "gqa_params.hpp"
+
+namespace gqa {
+
+namespace {
+
+constexpr int kDecD = 128;
+constexpr int kDecTileBytes = FwdStage<kDecD>::kTileBytes;  // one 64-key K or V tile: 16 KiB
+// Splits one combining thread requests per round (16-byte loads in flight).
+constexpr int kDecBatch = 32;
+// (row, split) pairs of m and l one combining thread loads (R * S <= 4096).
+constexpr int kDecMlPerThread = kFusedMaxRowSplitsHost / 256;
+
+// 16-byte device-coherent store (sc1: written through to the point where
+// all XCDs are coherent), through a buffer descriptor over the workspace.
+__device__ inline void store_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, 16);
+}
+
+// Fused log-sum-exp combine of the R valid rows of one (b, kv head, 32-row
+// block) over all S splits (gqa_split.py:134-147), by one workgroup:
+//   1. m and l of every (row, split), and the accumulators of this thread's
+//      first kDecBatch splits, are requested in one round; m and l go to
+//      LDS; per row (one wave, lanes over the splits) m* = max m, a = exp2(m
+//      - m*), l* = sum a * l;
+//   2. thread (split group sg, row, 4 columns) sums a * acc over splits sg,
+//      sg + nsg, ... (further rounds only beyond kDecBatch splits), the
+//      split groups are added in order in LDS, o = sum / l*.
+// Rows whose chunks are all empty give NaN (m* = -inf), as the reference's
+// combine; a sequence without keys (every split stores m = 0, l = 0) gives
+// zeros.  smem: >= (2 * R * S + 64) floats + nsg * R * D / 4 f32x4.
+template <int DT>
+__device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int t, char* smem) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  constexpr int D = kDecD, NDP = D / 4;
+  const Dims& dm = p.dm;
+  const int S = p.splits;
+  const int r0 = 32 * rb;
+  const int R = min(32, dm.G * dm.Sq - r0);
+  const int lane = t & 63, wave = t >> 6;
+  float* ma = reinterpret_cast<float*>(smem);  // [R][S]: m, then the scale factors a
+  float* la = ma + R * S;                      // [R][S]: l
+  float* mst = la + R * S;                     // [32]: m* per row
+  float* lst = mst + 32;                       // [32]: l* per row
+  f32x4* red = reinterpret_cast<f32x4*>(smem + (((2 * R * S + 64) * 4 + 15) & ~15));
+
+  auto row_index = [&](int rl) -> int64_t {  // workspace row of split 0
+    const int r = r0 + rl;
+    const int pos = r / dm.G, g = r - pos * dm.G;
+    return (((int64_t)b * dm.Hq + kvh * dm.G + g) * dm.Sq + pos) * S;
+  };
+  const int items = R * NDP;
+  const int nsg = items >= 256 ? 1 : max(1, min(S, 256 / items));
+  const int n_work = items * nsg;
+  // 16-byte loads through a descriptor over the whole acc workspace (the
+  // host bounds its size to 32-bit offsets).
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
+
+  // Round 1: m and l into registers, then this thread's first batch of
+  // accumulators, all in flight together.
+  float mreg[kDecMlPerThread], lreg[kDecMlPerThread];
+#pragma unroll
+  for (int k = 0; k < kDecMlPerThread; ++k) {
+    const int f = t + 256 * k;
+    if (f < R * S) {
+      const int rl = f / S, sp = f - rl * S;
+      const int64_t ix = row_index(rl) + sp;
+      mreg[k] = load_coherent(p.ws_m + ix);
+      lreg[k] = load_coherent(p.ws_l + ix);
+    }
+  }
+  f32x4 buf[kDecBatch];
+  int it = t;
+  int item = it % items, sg = it / items;
+  int rl = item / NDP, d4 = item - rl * NDP;
+  uint32_t base = (uint32_t)((row_index(rl) * D + 4 * d4) * 4);
+  if (it < n_work) {
+#pragma unroll
+    for (int k = 0; k < kDecBatch; ++k) {
+      const int sp = sg + k * nsg;
+      if (sp < S) buf[k] = load_coherent4(ra, base + (uint32_t)sp * (D * 4));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kDecMlPerThread; ++k) {
+    const int f = t + 256 * k;
+    if (f < R * S) {
+      ma[f] = mreg[k];
+      la[f] = lreg[k];
+    }
+  }
+  __syncthreads();
+  for (int rr = wave; rr < R; rr += 4) {
+    float m = -__builtin_inff();
+    for (int sp = lane; sp < S; sp += 64) m = fmaxf(m, ma[rr * S + sp]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    // exp2(-inf - -inf) = NaN when every chunk of a row is empty, as the
+    // reference's combine (gqa_split.py:138) gives.
+    float l = 0.f;
+    for (int sp = lane; sp < S; sp += 64) {
+      const float a = fast_exp2(ma[rr * S + sp] - m);
+      ma[rr * S + sp] = a;
+      l += a * la[rr * S + sp];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+    if (lane == 0) {
+      mst[rr] = m;
+      lst[rr] = l;
+      // LSE of a row with no visible key is -inf (its o stays NaN).
+      if (p.lse != nullptr)
+        p.lse[row_index(rr) / S] = m == -__builtin_inff() ? -__builtin_inff() : (m + __log2f(l)) * kLn2;
+    }
+  }
+  __syncthreads();
+
+  // Round 2 (and more only past kDecBatch splits per thread): a * acc.
+  for (bool first = true; it < n_work; it += 256, first = false) {
+    if (!first) {
+      item = it % items;
+      sg = it / items;
+      rl = item / NDP;
+      d4 = item - rl * NDP;
+      base = (uint32_t)((row_index(rl) * D + 4 * d4) * 4);
+    }
+    const float* a = ma + rl * S;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = sg; s0 < S; s0 += kDecBatch * nsg) {
+      if (!(first && s0 == sg)) {
+#pragma unroll
+        for (int k = 0; k < kDecBatch; ++k) {
+          const int sp = s0 + k * nsg;
+          if (sp < S) buf[k] = load_coherent4(ra, base + (uint32_t)sp * (D * 4));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kDecBatch; ++k) {
+        const int sp = s0 + k * nsg;
+        if (sp < S) o += a[sp] * buf[k];
+      }
+    }
+    red[it] = o;  // [sg][item]: it = sg * items + item
+  }
+  __syncthreads();
+  for (int f = t; f < items; f += 256) {
+    const int rl2 = f / NDP, d42 = f - (f / NDP) * NDP;
+    f32x4 o = red[f];
+    for (int g2 = 1; g2 < nsg; ++g2) o += red[g2 * items + f];
+    // A sequence without keys (finite m*, l* = 0, o = 0): 0 / inf = 0.
+    const float l = (lst[rl2] == 0.f && mst[rl2] > -__builtin_inff()) ? __builtin_inff() : lst[rl2];
+    const int r = r0 + rl2;
+    const int pos = r / dm.G, g = r - pos * dm.G;
+    T* orow = static_cast<T*>(const_cast<void*>(p.o.ptr)) + (int64_t)b * p.o.sb +
+              (int64_t)(kvh * dm.G + g) * p.o.sh + (int64_t)pos * p.o.ss + 4 * d42;
+    u32x2 x;
+    x[0] = E::pack2(o[0] / l, o[1] / l);
+    x[1] = E::pack2(o[2] / l, o[3] / l);
+    *reinterpret_cast<u32x2*>(orow) = x;
+  }
+}
+
+}  // namespace
+
+template <int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_decode_kernel(SplitParams p) {
+  constexpr int D = kDecD;
+  using E = Elem<DT>;
+  using T = typename E::T;
+  using ST = FwdStage<D>;
+  constexpr int CPR = ST::CPR;
+  constexpr int NKS = D / 16;  // k-steps of S^T
+  constexpr int NI = ST::NI;   // LDS-DMA instructions per wave per K (or V) tile
+  // Four separate arrays (K and V of two stages), not one: the compiler can
+  // then tell the LDS-DMA target of the tile in flight from the stage being
+  // read and does not wait for those loads before the reads.  The combine
+  // reuses all four as one 64 KiB area (the compiler lays them out in name
+  // order, back to back).
+  __shared__ __attribute__((aligned(1024))) char lds_a_k0[kDecTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b_v0[kDecTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_c_k1[kDecTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_d_v1[kDecTileBytes];
+  __shared__ int s_last;
+
+  const Dims& dm = p.dm;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;  // also this wave's 32-dim block of O^T
+  const int i = lane & 31, hh = lane >> 5;
+
+  const int total = dm.B * dm.Hkv * p.n_rblk * p.splits;
+  const int w = xcd_remap(blockIdx.x, total);
+  const int s = w % p.splits;
+  int rest = w / p.splits;
+  const int rb = rest % p.n_rblk;
+  rest /= p.n_rblk;
+  const int kvh = rest % dm.Hkv;
+  const int b = rest / dm.Hkv;
+  const int skv = dm.Skv, sq = dm.Sq;
+
+  // This lane's query row (position-major packing).
+  const int r = 32 * rb + i;
+  const int pos = r / dm.G, g = r - pos * dm.G;
+  const bool valid = pos < sq;
+  const int head = kvh * dm.G + g;
+  const int qpos = pos + (skv - sq);
+
+  // Keys of this chunk (gqa_split.py:55-60), clamped to the block's last
+  // visible key under causal.
+  const int c0 = s * p.chunk;
+  int c1 = min(c0 + p.chunk, skv);
+  const int pos_lo = (32 * rb) / dm.G;
+  const int pos_hi = min(sq - 1, (32 * rb + 31) / dm.G);
+  if (dm.causal) c1 = min(c1, pos_hi + (skv - sq) + 1);
+  const int nk = max(c1 - c0, 0);
+  const int ntiles = (nk + 63) >> 6;
+  const int qpos_lo = pos_lo + (skv - sq);
+
+  // Buffer descriptors over the chunk's K and V rows, each ending at the
+  // chunk's last key: rows of a partial last tile past it read as zero (and
+  // are masked).  The host bounds (chunk + 64) * row stride to 31 bits.
+  const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
+  const char* kbase = static_cast<const char*>(p.k.ptr) +
+                      2 * ((int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh + (int64_t)c0 * p.k.ss);
+  const char* vbase = static_cast<const char*>(p.v.ptr) +
+                      2 * ((int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh + (int64_t)c0 * p.v.ss);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, nk > 0 ? (uint32_t)(nk - 1) * kssb + 2 * D : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, nk > 0 ? (uint32_t)(nk - 1) * vssb + 2 * D : 0u);
+
+  // Tile order.  With one head's keys in consecutive rows, every workgroup
+  // would otherwise stream its chunk from the same relative offset in lock
+  // step with the others, concentrating the concurrent reads on a subset of
+  // the HBM channels; splits s = 0..3 (mod 4) start a quarter of the chunk
+  // apart.  The online softmax does not depend on the order.
+  // Tiles past the chunk (the prologue's tiles of a chunk shorter than two,
+  // the padding of an odd count) are not rotated: they lie beyond the
+  // descriptors, read as zero and are fully masked.
+  const int rot = (p.rotate && ntiles >= 4) ? (s & 3) * (ntiles >> 2) : 0;
+  auto tile_rel = [&](int it) {
+    const int j = it + rot;
+    return it >= ntiles ? it : (j >= ntiles ? j - ntiles : j);
+  };
+
+  // LDS-DMA source offsets of this lane (its row within an instruction's 4
+  // rows, its swizzled chunk), as the single pass.
+  const int lrow = lane / CPR;
+  const uint32_t koff =
+      (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ ST::gk((wave * ST::RPI + lrow) & 15));
+  const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ ST::sv(lrow));
+  // The prologue issues tiles 0 and 1 unconditionally (a tile past the
+  // chunk reads zeros); the loop issues a tile only if it exists.
+  auto issue = [&](int it, char* kst, char* vst) {
+    const uint32_t j = (uint32_t)tile_rel(it) * 64u;
+    issue_tile_dma<D, kDmaStream>(kst, rk, j * kssb, kssb, koff, wave);
+    issue_tile_dma<D, kDmaStream>(vst, rv, j * vssb, vssb, voff, wave);
+  };
+
+  // Loads in issue order: tile 0, Q, tile 1 (the wait for tile 0 and Q then
+  // leaves tile 1 in flight).  Only lanes of valid rows load Q (a decode
+  // step has 4 of 32): the others would re-request the same rows from L2 in
+  // every wave of every workgroup, beside the K/V stream.
+  // (Through a descriptor over this kv head's query group: an invalid
+  // lane's offset lies past its end and reads zero without a memory access,
+  // and no branch splits the wave.)
+  issue(0, lds_a_k0, lds_b_v0);
+  u32x4 qreg[NKS];
+  {
+    const char* qg = static_cast<const char*>(p.q.ptr) + 2 * ((int64_t)b * p.q.sb + (int64_t)kvh * dm.G * p.q.sh);
+    const uint32_t qext = (uint32_t)(2 * ((int64_t)(dm.G - 1) * p.q.sh + (int64_t)(sq - 1) * p.q.ss + D));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(qg, qext);
+    const uint32_t qo = valid ? (uint32_t)(2 * ((int64_t)g * p.q.sh + (int64_t)pos * p.q.ss) + 16 * hh) : 0x80000000u;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      qreg[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 32u * ks, 0, 0));
+  }
+  issue(1, lds_c_k1, lds_d_v1);
+  // Tile 0 and Q have landed (tile 1 may still be in flight).  Waiting here,
+  // explicitly, also settles Q for the compiler: otherwise it waits for
+  // every load in flight before entering the tile loop.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NI));
+
+  // LDS read offsets: S^T A operand (K rows pi(i)), V^T A operand of this
+  // wave's dims (transposing reads), as the single pass.
+  constexpr uint32_t kKMask = (kDecTileBytes / 2 - 1) & ~15u;
+  constexpr uint32_t kVMask = (kDecTileBytes - 1) & ~7u;
+  uint32_t ka[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+    ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
+  uint32_t vb;
+  {
+    const int q = lane >> 4, ii = lane & 15;
+    const int rowl = 8 * (q >> 1) + (ii >> 2);
+    const int f = ii >> 2;  // sv(rowl) / 4
+    vb = (uint32_t)(rowl * (2 * D) + 16 * (4 * (wave ^ f) + 2 * (q & 1) + ((ii & 3) >> 1)) + 8 * (ii & 1)) & kVMask;
+  }
+
+  f32x16 acc = {};
+  float m_run = -__builtin_inff(), l_run = 0.f;
+  const float c = dm.c;
+
+  // Issue priority falls with progress (3 for the first quarter of the
+  // chunk, then 2, 1, 0): two workgroups share a compute unit, and ranking
+  // by progress keeps them within a quarter of each other instead of the
+  // older one streaming ahead and the younger one finishing alone.
+  auto set_prio = [&](int it) {
+    const int lvl = (4 * it) / ntiles;
+    if (lvl == 0) __builtin_amdgcn_s_setprio(3);
+    else if (lvl == 1) __builtin_amdgcn_s_setprio(2);
+    else if (lvl == 2) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+  };
+
+  // One 64-key tile from stage S3 (tile it of this chunk's order); with
+  // ISSUE, the stage is then refilled with tile it + 2; LAST: no tile is in
+  // flight behind this one.  Both are compile-time decisions: a run-time
+  // condition around the issue makes the compiler's own wait tracking merge
+  // the two paths and wait for every load in flight before the next LDS
+  // reads.
+  auto step = [&](auto s3, auto issue_c, auto last_c, int it) {
+    constexpr int S3 = decltype(s3)::value;
+    constexpr bool ISSUE = decltype(issue_c)::value;
+    constexpr bool LAST = decltype(last_c)::value;
+    char* kst = S3 == 0 ? lds_a_k0 : lds_c_k1;
+    char* vst = S3 == 0 ? lds_b_v0 : lds_d_v1;
+    const char* ck = kst;
+    const char* cv = vst;
+    if ((it & 3) == 0) set_prio(it);
+    // This wave's loads of tile it have landed (those of tile it + 1 may
+    // still be in flight); after the barrier, every wave's have.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LAST ? 0 : 2 * NI));
+    phase_barrier();
+
+    // S^T for the 64 keys: two 32-key blocks, NKS k-steps each.
+    f32x16 sc[2] = {f32x16{}, f32x16{}};
+    {
+      u32x4 opk[2 * NKS];
+#pragma unroll
+      for (int j = 0; j < 2 * NKS; ++j) opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + ka[j >> 1]);
+#pragma unroll
+      for (int j = 0; j < 2 * NKS; ++j) sc[j & 1] = E::mfma(opk[j], qreg[j >> 1], sc[j & 1]);
+    }
+    const int key0 = c0 + tile_rel(it) * 64;
+    const bool need_mask = (key0 + 64 > c1) || (dm.causal && key0 + 63 > qpos_lo);
+    if (need_mask) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = key0 + 32 * mb + key_of(v, hh);
+          const bool off = key >= c1 || (dm.causal && key > qpos);
+          sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
+        }
+    }
+    // Exact online softmax (gqa_split.py:92-101) in exp2 units; a row with
+    // no visible key so far keeps m = -inf and uses 0 as reference, so its
+    // probabilities are 0, never NaN.
+    float m1[11];
+#pragma unroll
+    for (int k = 0; k < 10; ++k) {
+      const int i0 = 3 * k, i1 = 3 * k + 1, i2 = 3 * k + 2;
+      m1[k] = vmax3(sc[i0 >> 4][i0 & 15], sc[i1 >> 4][i1 & 15], sc[i2 >> 4][i2 & 15]);
+    }
+    m1[10] = vmax3(sc[1][14], sc[1][15], sc[1][15]);
+    const float n0 = vmax3(m1[0], m1[1], m1[2]), n1 = vmax3(m1[3], m1[4], m1[5]);
+    const float n2 = vmax3(m1[6], m1[7], m1[8]), n3 = vmax3(m1[9], m1[10], m1[10]);
+    const float mx = xhalf_max(vmax3(vmax3(n0, n1, n2), n3, n3));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = fast_exp2((m_run - m_use) * c);
+    const float nmc = -m_use * c;
+    u32x4 pk[2][2];
+    float rs = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      float pv[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) pv[v] = fast_exp2(__builtin_fmaf(sc[mb][v], c, nmc));
+      float s8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s8[j] = pv[2 * j] + pv[2 * j + 1];
+      rs += ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pk[mb][kk][e] = E::pack2(pv[8 * kk + 2 * e], pv[8 * kk + 2 * e + 1]);
+    }
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] *= alpha;
+
+    // O^T (this wave's 32 dims) += V^T P^T over the 64 keys.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int mb = j >> 1, kk = j & 1;
+      const int ro = (32 * mb + 16 * kk) * (2 * D);
+      const u32x2 lo = ld_tr(cv + vb + ro);
+      const u32x2 hi = ld_tr(cv + vb + ro + 4 * (2 * D));
+      acc = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[mb][kk], acc);
+    }
+    // Every wave is done with this stage: refill it with the tile two ahead.
+    phase_barrier();
+    if constexpr (ISSUE) issue(it + 2, kst, vst);
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using BT = std::true_type;
+  using BF = std::false_type;
+  // Tiles in pairs (stage 0, stage 1); an odd count is padded with one tile
+  // past the chunk (zeros, every key masked: it adds nothing).
+  const int ne = (ntiles + 1) & ~1;
+  int it = 0;
+  for (; it + 4 <= ne; it += 2) {
+    step(I0{}, BT{}, BF{}, it);
+    step(I1{}, BT{}, BF{}, it + 1);
+  }
+  if (it < ne) {
+    step(I0{}, BF{}, BF{}, it);
+    step(I1{}, BF{}, BT{}, it + 1);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  // Nothing is left in flight (an empty chunk still issued the prologue's
+  // two tiles of zeros) before the workgroup exits or the combine reuses the
+  // stages.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // This wave's 32 dims of the valid rows' partials: lane (i, hh) holds
+  // dims 32 * wave + 8 * j + 4 * hh + 0..3 in acc[4j .. 4j + 3].
+  const float l_tot = xhalf_sum(l_run);
+  if (valid) {
+    const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
+    const uint32_t ob = (uint32_t)((row * D + 32 * wave + 4 * hh) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      store_coherent4(rw, ob + 32u * j, f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]});
+    // A sequence without keys stores m = 0, l = 0 (never produced otherwise:
+    // the chunk's largest score contributes exp2(0) = 1 to l), which the
+    // combine turns into a zero row.
+    if (wave == 0 && hh == 0) {
+      store_coherent(p.ws_m + row, skv == 0 ? 0.f : m_run * c);
+      store_coherent(p.ws_l + row, l_tot);
+    }
+  }
+
+  if (p.counters == nullptr) return;
+  // Fused combine: count this partial once its stores have completed; the
+  // workgroup completing the count for this (b, kv head, row block) combines.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const int idx = (b * dm.Hkv + kvh) * p.n_rblk + rb;
+    const int prev = __hip_atomic_fetch_add(&p.counters[idx], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == p.splits - 1);
+    // Every increment of this call has landed: leave the counter zero.
+    if (s_last) __hip_atomic_store(&p.counters[idx], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  decode_combine<DT>(p, b, kvh, rb, t, lds_a_k0);
+}
+
+bool decode_kernel_fits(const SplitParams& p) {
+  if (p.dm.D != kDecD || p.block_table != nullptr || p.q_len != nullptr) return false;
+  // 32-bit descriptor offsets: a chunk (plus a tile) of K and V rows, and
+  // the whole accumulator workspace.
+  const int64_t span = (int64_t)p.chunk + 64;
+  if (span * p.k.ss * 2 >= ((int64_t)1 << 31) || span * p.v.ss * 2 >= ((int64_t)1 << 31)) return false;
+  const int64_t acc_bytes = (int64_t)p.dm.B * p.dm.Hq * p.dm.Sq * p.splits * kDecD * 4;
+  // ... and a kv head's query group (its G heads x Sq rows).
+  const int64_t q_bytes = 2 * ((int64_t)(p.dm.G - 1) * p.q.sh + (int64_t)(p.dm.Sq - 1) * p.q.ss + kDecD);
+  return acc_bytes <= 0xFFFFFFF0ll && q_bytes < ((int64_t)1 << 31);
+}
+
+template <int DT>
+static hipError_t launch_decode_t(const SplitParams& p, hipStream_t stream) {
+  const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * p.n_rblk * p.splits;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL((gqa_decode_kernel<DT>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_first(const SplitParams& p, int dtype, hipStream_t stream) {
+  return dtype == 0 ? launch_decode_t<0>(p, stream) : launch_decode_t<1>(p, stream);
+}
+
+}  // namespace gqa

@@ -136,5 +136,9 @@ hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t strea
 hipError_t launch_paged_split_first(const SplitParams& p, int dtype, hipStream_t stream);
 hipError_t launch_paged_cache_write(const CacheWriteParams& p, hipStream_t stream);
 hipError_t launch_split_reduce(const ReduceParams& p, int dtype, hipStream_t stream);
+// Decode-shaped first pass (gqa_decode.hip): head_dim 128, contiguous K/V,
+// fixed query lengths, 32-bit chunk and workspace offsets.
+bool decode_kernel_fits(const SplitParams& p);
+hipError_t launch_decode_first(const SplitParams& p, int dtype, hipStream_t stream);  // fused if p.counters
 
 }  // namespace gqa

@@ -412,16 +412,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // LSE combine.  256 threads: thread (d4, sg) owns output columns
-// [4*d4, 4*d4 + 4) and the splits sg, sg + NSG, ...
-template <int DT, int D>
+// [4*d4, 4*d4 + 4) and the splits sg, sg + NSG, ...  One round of loads:
+// each thread requests m, l and the accumulators of its splits together
+// (up to BATCH splits at a time: 1 when every thread has at most one split,
+// else 8) and combines them against its own running maximum; the NSG split
+// groups are then merged in LDS against the row maximum m*:
+//   m* = max m_s, a_s = exp2(m_s - m*), l* = sum a_s l_s,
+//   o = sum a_s acc_s / l*                           (gqa_split.py:134-147)
+template <int DT, int D, int BATCH>
 __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
+  constexpr int kReduceBatch = BATCH;
   using E = Elem<DT>;
   using T = typename E::T;
   constexpr int ND4 = D / 4;
   constexpr int NSG = 256 / ND4;
-  __shared__ float red_m[4];
-  __shared__ f32x4 red_o[NSG][ND4];
+  __shared__ float red_m[NSG][ND4];
   __shared__ float red_l[NSG][ND4];
+  __shared__ f32x4 red_o[NSG][ND4];
 
   const int t = threadIdx.x;
   const int row = blockIdx.x;  // ((b * Hq + h) * Sq + pos)
@@ -438,35 +445,57 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   const float* wl = p.ws_l + (int64_t)row * S;
   const float* wa = p.ws_acc + (int64_t)row * S * D;
 
-  // m* = max over splits: per-thread max, wave max, then the 4 waves in LDS.
-  float mx = -__builtin_inff();
-#pragma unroll 4
-  for (int s = t; s < S; s += 256) mx = fmaxf(mx, wm[s]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((t & 63) == 0) red_m[t >> 6] = mx;
-  __syncthreads();
-  const float mstar = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-
-  // Thread (d4, sg) sums its splits sg, sg + NSG, ...; unrolled so that the
-  // loads of several splits are in flight together.
   const int d4 = t % ND4, sg = t / ND4;
+  float m_loc = -__builtin_inff(), l_loc = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-#pragma unroll 8
-  for (int s = sg; s < S; s += NSG) {
-    // exp2(-inf - -inf) = NaN when every chunk is empty, as gqa_split.py:138.
-    const float a = fast_exp2(wm[s] - mstar);
-    l += a * wl[s];
-    o += a * *reinterpret_cast<const f32x4*>(wa + (int64_t)s * D + 4 * d4);
+  for (int s0 = sg; s0 < S; s0 += kReduceBatch * NSG) {
+    float mv[kReduceBatch], lv[kReduceBatch];
+    f32x4 av[kReduceBatch];
+#pragma unroll
+    for (int k = 0; k < kReduceBatch; ++k) {
+      const int s = s0 + k * NSG;
+      mv[k] = -__builtin_inff();
+      lv[k] = 0.f;
+      av[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (s < S) {
+        mv[k] = wm[s];
+        lv[k] = wl[s];
+        av[k] = *reinterpret_cast<const f32x4*>(wa + (int64_t)s * D + 4 * d4);
+      }
+    }
+    float mb = m_loc;
+#pragma unroll
+    for (int k = 0; k < kReduceBatch; ++k) mb = fmaxf(mb, mv[k]);
+    // Nothing visible yet (every split so far empty): keep (-inf, 0, 0).
+    if (mb == -__builtin_inff()) continue;
+    const float r = fast_exp2(m_loc - mb);  // 0 while m_loc is -inf
+    l_loc *= r;
+    o *= r;
+#pragma unroll
+    for (int k = 0; k < kReduceBatch; ++k) {
+      const float a = fast_exp2(mv[k] - mb);
+      l_loc += a * lv[k];
+      o += a * av[k];
+    }
+    m_loc = mb;
   }
+  red_m[sg][d4] = m_loc;
+  red_l[sg][d4] = l_loc;
   red_o[sg][d4] = o;
-  red_l[sg][d4] = l;
   __syncthreads();
   if (sg == 0) {
-    for (int k = 1; k < NSG; ++k) {
-      o += red_o[k][d4];
-      l += red_l[k][d4];
+    float mstar = red_m[0][d4];
+#pragma unroll
+    for (int k = 1; k < NSG; ++k) mstar = fmaxf(mstar, red_m[k][d4]);
+    // exp2(-inf - -inf) = NaN when every chunk is empty, as gqa_split.py:138;
+    // a group with no visible key (m = -inf, l = 0, o = 0) adds nothing.
+    float l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < NSG; ++k) {
+      const float a = fast_exp2(red_m[k][d4] - mstar);
+      l += a * red_l[k][d4];
+      acc += a * red_o[k][d4];
     }
     // Optional LSE side output (natural log; m* and l* are log2-domain);
     // -inf for a row with no visible key (whose o stays NaN).
@@ -479,8 +508,8 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
     // A sequence without keys (finite m*, l* = 0, o = 0): 0 / inf = 0.
     if (l == 0.f && mstar > -__builtin_inff()) l = __builtin_inff();
     u32x2 x;
-    x[0] = E::pack2(o[0] / l, o[1] / l);
-    x[1] = E::pack2(o[2] / l, o[3] / l);
+    x[0] = E::pack2(acc[0] / l, acc[1] / l);
+    x[1] = E::pack2(acc[2] / l, acc[3] / l);
     *reinterpret_cast<u32x2*>(orow + 4 * d4) = x;
   }
 }
@@ -497,11 +526,15 @@ template <int DT, int D>
 static hipError_t launch_split_reduce_t(const ReduceParams& p, hipStream_t stream) {
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_split_reduce_kernel<DT, D>), dim3((unsigned)rows), dim3(256), 0, stream, p);
+  if (p.splits <= 256 / (D / 4))  // at most one split per thread
+    hipLaunchKernelGGL((gqa_split_reduce_kernel<DT, D, 1>), dim3((unsigned)rows), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gqa_split_reduce_kernel<DT, D, 8>), dim3((unsigned)rows), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream) {
+  if (decode_kernel_fits(p)) return launch_decode_first(p, dtype, stream);
   if (dtype == 0)
     return p.dm.D == 128 ? launch_split_first_t<0, 128, 0>(p, stream) : launch_split_first_t<0, 64, 0>(p, stream);
   return p.dm.D == 128 ? launch_split_first_t<1, 128, 0>(p, stream) : launch_split_first_t<1, 64, 0>(p, stream);
