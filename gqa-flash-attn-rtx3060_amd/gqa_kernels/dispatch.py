@@ -16,7 +16,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .gqa_split import _counter_buffer, _workspace_buffer, split_kv_forward, stream_handle
+from .gqa_split import _counter_buffer, _workspace_buffer, decode_forward, stream_handle
 
 __all__ = ["gqa_flash_attn", "Route", "choose_route"]
 
@@ -213,15 +213,23 @@ def gqa_flash_attn(q, k, v, causal=True, *, return_lse=False):
 
     route = _route_cached(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev), bool(causal))
     if dev == torch.cuda.current_device():
-        return _launch(route, q, k, v, causal, return_lse)
+        return _launch(route, q, k, v, causal, return_lse, dev)
     with torch.cuda.device(dev):  # launch on q's device
-        return _launch(route, q, k, v, causal, return_lse)
+        return _launch(route, q, k, v, causal, return_lse, dev)
 
 
-def _launch(route, q_in, k, v, causal, return_lse):
-    q, k, v = _kernel_ready(q_in), _kernel_ready(k), _kernel_ready(v)
+def _launch(route, q_in, k, v, causal, return_lse, dev):
+    # One test for the usual case (all three kernel-ready; 2-byte elements:
+    # the dtype is asserted), the per-tensor copies otherwise.
+    qs, ks, vs = q_in.stride(), k.stride(), v.stride()
+    if (qs[3] == 1 and ks[3] == 1 and vs[3] == 1
+            and ((q_in.data_ptr() | k.data_ptr() | v.data_ptr()
+                  | 2 * (qs[0] | qs[1] | qs[2] | ks[0] | ks[1] | ks[2] | vs[0] | vs[1] | vs[2])) & 15) == 0):
+        q = q_in
+    else:
+        q, k, v = _kernel_ready(q_in), _kernel_ready(k), _kernel_ready(v)
     if route.kind == "split":
-        return split_kv_forward(q, k, v, causal, route.splits, return_lse=return_lse)
+        return decode_forward(q, k, v, causal, route.splits, return_lse, dev)
     o = torch.empty_like(q_in)  # as dispatch.py:47; contiguous if unusable
     if not _is_kernel_ready(o):
         o = torch.empty_like(q_in, memory_format=torch.contiguous_format)

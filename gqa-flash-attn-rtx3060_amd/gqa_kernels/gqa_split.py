@@ -16,7 +16,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["split_kv_forward", "workspace_bytes", "stream_handle"]
+__all__ = ["split_kv_forward", "decode_forward", "workspace_bytes", "stream_handle"]
 
 # Zeroed int32 counters for the fused combine, one buffer per (device,
 # stream): the kernel leaves them zero, so a buffer is reused by every call on
@@ -90,6 +90,34 @@ _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 def workspace_bytes(batch: int, num_heads: int, seq_q: int, head_dim: int, splits: int) -> int:
     """fp32 workspace size: acc (B,Hq,Sq,S,D) then m and l (B,Hq,Sq,S)."""
     return batch * num_heads * seq_q * splits * (head_dim + 2) * 4
+
+
+_SCALE_LOG2 = {64: 64 ** -0.5 * LOG2E, 128: 128 ** -0.5 * LOG2E}
+
+
+def decode_forward(q, k, v, causal, splits, return_lse, dev):
+    """The two-launch split-KV forward as gqa_flash_attn takes it: kernel-ready
+    q, k, v on device index `dev` (the current device), the stream's cached
+    workspace.  Computes exactly what split_kv_forward(q, k, v, causal,
+    splits, return_lse=return_lse) does, with the host work of a decode step
+    kept to one pass over the arguments (every value read once)."""
+    batch, num_heads, seq_q, head_dim = q.shape
+    _, num_kv_heads, seq_kv, _ = k.shape
+    stream = _raw_stream(dev) if _raw_stream is not None else torch.cuda.current_stream(dev).cuda_stream
+    need = batch * num_heads * seq_q * splits * (head_dim + 2) * 4
+    ws = _workspaces.get((dev, stream))
+    if ws is None or ws.numel() * 4 < need:
+        ws = _workspace_buffer(q.device, stream, need)
+    o = torch.empty_like(q)
+    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
+    rc = _lib.load().gqa_split_launch(
+        q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k), v.data_ptr(), _lib.strides(v),
+        o.data_ptr(), _lib.strides(o), None if lse is None else lse.data_ptr(), ws.data_ptr(), splits,
+        batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, _SCALE_LOG2[head_dim], 1 if causal else 0,
+        _DTYPES[q.dtype], stream)
+    if rc:
+        _lib.check(rc)
+    return o if lse is None else (o, lse)
 
 
 def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False, return_lse=False):
