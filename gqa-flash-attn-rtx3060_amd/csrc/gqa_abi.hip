@@ -22,7 +22,10 @@ using gqa::TensorRef;
 // GQA_PAGED_CHUNK_PAGES pages (GQA_E_SPLITS beyond); a sequence without keys
 // gives zero rows on every path.  8: gqa_split_noalloc_launch.
 // 9: gqa_split_launch (first pass and combine in one call).
-constexpr int kAbiVersion = 9;
+// 10: gqa_fwd_split_counters_count adds the persistent single pass's
+// scheduling counters (also for n_split = 0); gqa_fwd_split_launch with
+// counters schedules the work items across the XCDs dynamically.
+constexpr int kAbiVersion = 10;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -123,9 +126,9 @@ int fwd_impl(const void* q, const int64_t q_stride[4], const void* k, const int6
   if (batch == 0 || seq_q == 0) return GQA_OK;
   if (n_split > 0) {
     if (part_ws == nullptr || part_cnt == nullptr) return GQA_E_NULL;
-    if ((reinterpret_cast<uintptr_t>(part_ws) & 15u) != 0 || (reinterpret_cast<uintptr_t>(part_cnt) & 3u) != 0)
-      return GQA_E_STRIDE;
+    if ((reinterpret_cast<uintptr_t>(part_ws) & 15u) != 0) return GQA_E_STRIDE;
   }
+  if ((reinterpret_cast<uintptr_t>(part_cnt) & 3u) != 0) return GQA_E_STRIDE;
   if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
   if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
   if (seq_kv > 0 && (!rows_fit_32bit(seq_kv, k_stride) || !rows_fit_32bit(seq_kv, v_stride))) return GQA_E_STRIDE;
@@ -142,6 +145,8 @@ int fwd_impl(const void* q, const int64_t q_stride[4], const void* k, const int6
   p.n_split = n_split;
   p.part_ws = part_ws;
   p.part_cnt = part_cnt;
+  // The scheduling counters follow the split blocks' counters.
+  p.sched = part_cnt != nullptr ? part_cnt + (size_t)batch * num_kv_heads * n_split : nullptr;
   return to_code(gqa::launch_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
@@ -186,8 +191,8 @@ size_t gqa_fwd_split_workspace_bytes(int batch, int num_kv_heads, int head_dim, 
 }
 
 size_t gqa_fwd_split_counters_count(int batch, int num_kv_heads, int n_split) {
-  if (batch <= 0 || num_kv_heads <= 0 || n_split <= 0) return 0;
-  return (size_t)batch * num_kv_heads * n_split;
+  if (batch <= 0 || num_kv_heads <= 0 || n_split < 0) return 0;
+  return (size_t)batch * num_kv_heads * n_split + gqa::kFwdSchedCounters;
 }
 
 int gqa_fwd_split_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],

@@ -199,16 +199,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // (round j: slot c takes item j*S + c, or j*S + S-1-c in odd rounds), so
   // the heavy-first order hands every slot a mix of heavy and light items.
   const int n_wg = PERSIST ? p.n_wg : total;
+  // Item range of XCD x: [lo, lo + n), served by its S workgroups.
+  auto xrange = [&](int x, int& lo, int& n, int& S) {
+    S = (n_wg - x + 7) >> 3;
+    const int q = total >> 3, r = total & 7;
+    lo = x * q + min(x, r);
+    n = q + (x < r ? 1 : 0);
+  };
   auto item_at = [&](int k) -> int {
     if (!PERSIST) return k == 0 ? xcd_remap(blockIdx.x, total) : -1;
     const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
-    const int S = (n_wg - x + 7) >> 3;  // workgroups on XCD x
-    const int q = total >> 3, r = total & 7;
-    const int lo = x * q + min(x, r), n = q + (x < r ? 1 : 0);
+    int lo, n, S;
+    xrange(x, lo, n, S);
     const int j = k;
     const int e = j * S + ((j & 1) ? S - 1 - slot : slot);
     return e < n ? lo + e : -1;
   };
+  // Dynamic schedule (persistent kernel, p.sched set): the XCDs run at
+  // different speeds under sustained MFMA load (their workgroups end up to
+  // 6 % apart on a static schedule), so after its first item (slot c of XCD
+  // x takes item c of x's range, as above) a workgroup claims the next one
+  // from its own XCD's queue — items S, S + 1, ... of the range, heavy
+  // first — and, once that is empty, from the other XCDs' queues.  One
+  // thread claims with an agent-scope atomic issued as the epilogue begins
+  // and resolves it after the output stores, so its latency is hidden.
+  // Items are independent (a split block's halves merge in a fixed order),
+  // so the outputs do not depend on who computes what.  p.sched: 8 queue
+  // counters, 8 + 1 counts of workgroups done, zero on entry; the last
+  // workgroup to finish leaves them zero.  The counters' address waits in
+  // LDS (kept in registers, it would add to those held across the tile
+  // loop).
+  __shared__ int s_next;
+  __shared__ int* s_sched;
+  if (PERSIST && t == 0) s_sched = p.sched;
 
   // One work item's parameters.
   struct Item {
@@ -610,7 +633,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
 
-    const int w_next = PERSIST ? item_at(k_item + 1) : -1;
+    int* sched = nullptr;
+    if constexpr (PERSIST) sched = s_sched;
+    const bool dyn = sched != nullptr;
+    int w_next = PERSIST && !dyn ? item_at(k_item + 1) : -1;
+    // Dynamic schedule: thread 0 claims a ticket of this XCD's queue as the
+    // epilogue begins; it is resolved after the output stores, which hide
+    // the atomic's round trip.
+    const int xq = (int)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 7);  // HW_REG_XCC_ID
+    int ticket = 0;
+    if (dyn && t == 0) ticket = __hip_atomic_fetch_add(&sched[xq], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // One workgroup per item: this item's parameters and the lane ids again,
     // from the item index, block_m and a zero laundered through SGPRs (the
     // lane id through v_mbcnt): kept from the start, the values read only
@@ -738,6 +770,55 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
         }
       }
     }
+    if (dyn) {
+      if (wave == 0) {
+        int lo, n, S;
+        xrange(xq, lo, n, S);
+        int w = __builtin_amdgcn_readfirstlane(S + ticket < n ? lo + S + ticket : -1);
+        // This XCD's queue is empty: lanes 1-7 read the other queues'
+        // counters at once; the first one with items left is claimed (a
+        // failed claim means that queue has just run out: counters only
+        // grow, so at most 7 rounds).
+        for (int round = 0; round < 8 && w < 0; ++round) {
+          const int y = (xq + lane) & 7;
+          int ly, ny, Sy;
+          xrange(y, ly, ny, Sy);
+          int left = 0;
+          if (lane >= 1 && lane < 8 && Sy < ny)
+            left = ny - Sy - __hip_atomic_load(&sched[y], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint64_t has = __builtin_amdgcn_ballot_w64(left > 0);
+          if (has == 0) break;  // every queue is empty
+          const int d = __builtin_ffsll((long long)has) - 1;
+          const int yc = (xq + d) & 7;
+          int lc, nc, Sc;
+          xrange(yc, lc, nc, Sc);
+          int tk = 0;
+          if (lane == 0) tk = __hip_atomic_fetch_add(&sched[yc], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          tk = __builtin_amdgcn_readfirstlane(tk);
+          if (Sc + tk < nc) w = lc + Sc + tk;
+        }
+        if (w < 0 && lane == 0) {
+          // No work left: count out, in two levels so that the workgroups
+          // ending together do not all queue on one counter: the S
+          // workgroups of group g = blockIdx % 8, then the groups.  The
+          // last workgroup out has seen every other workgroup's claims
+          // complete: it clears the counters.
+          const int g = blockIdx.x & 7;
+          int lg, ng, Sg;
+          xrange(g, lg, ng, Sg);
+          const int dg = __hip_atomic_fetch_add(&sched[8 + g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (dg == Sg - 1) {
+            const int groups = min(n_wg, 8);
+            const int dt = __hip_atomic_fetch_add(&sched[16], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (dt == groups - 1)
+              for (int z = 0; z < 17; ++z) __hip_atomic_store(&sched[z], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        if (lane == 0) s_next = w;
+      }
+      __syncthreads();
+      w_next = s_next;
+    }
     if (!PERSIST || w_next < 0) break;
     // Persistent: the next item's first tiles (once every wave's output has
     // left the stages) and Q, loaded while the output stores drain.
@@ -771,6 +852,14 @@ static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
     const int cus = device_cu_count();
     grid = cus > 0 ? std::min(total, cus) : total;
     p.n_wg = grid;
+    // The dynamic schedule pays for its claims (atomic round trips of ~2 us,
+    // and a tail of them as the last workgroups finish) only with many
+    // items per workgroup: measured -0.5 to -1.1 % at 8 (16K-token
+    // prefill), +1 to +3 % at 2-4 and +25 % at 1-2 (key-split short
+    // prefill); below 8 the static snake schedule runs.
+    if (total < kFwdDynMinItemsPerWg * grid) p.sched = nullptr;
+  } else {
+    p.sched = nullptr;
   }
   hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();

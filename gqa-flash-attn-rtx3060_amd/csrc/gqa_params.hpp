@@ -50,6 +50,9 @@ struct FwdParams {
   // Persistent single pass (contiguous K/V, head_dim 128): workgroups
   // launched, each working through a list of items (set by launch_fwd).
   int n_wg;
+  // Persistent single pass: nullptr (static schedule) or kFwdSchedCounters
+  // zero-initialised ints (dynamic schedule across XCDs), left zero.
+  int* sched;
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).
@@ -106,6 +109,11 @@ constexpr int kFwdThreads = 512;
 // One partial state of a split query block: per lane of the 8 waves, D/2
 // accumulators, the reference max and the lane's partial row sum.
 constexpr int kFwdPartFloats(int D) { return kFwdThreads * (D / 2 + 2); }
+// Scheduling counters of the persistent single pass (8 XCD queues, 8 + 1
+// counts of finished workgroups, padding), and the items per workgroup from
+// which it schedules dynamically.
+constexpr int kFwdSchedCounters = 32;
+constexpr int kFwdDynMinItemsPerWg = 8;
 // ln(2): converts a log2-domain log-sum-exp to the natural-log LSE.
 constexpr float kLn2 = 0.693147180559945309f;
 // Keys per single-pass LDS tile, and per split-KV LDS tile.

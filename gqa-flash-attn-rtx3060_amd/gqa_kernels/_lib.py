@@ -21,7 +21,7 @@ GQA_MAX_BLOCK_SIZE = 65536
 GQA_PAGED_CHUNK_PAGES = 2048
 GQA_NOALLOC_SCRATCH_BYTES = 16 << 20
 GQA_E_SCRATCH = -9
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3

@@ -237,9 +237,10 @@ def _launch(route, q_in, k, v, causal, return_lse, dev):
 
 
 def single_pass_forward(q, k, v, o, causal, fwd_split=0, return_lse=False):
-    """Launch the single-pass kernel on kernel-ready q, k, v and output o;
-    with fwd_split > 0 the heaviest query blocks run as two key halves
-    (gqa_fwd_split_launch; workspace and counters are the stream's cached
+    """Launch the single-pass kernel on kernel-ready q, k, v and output o
+    through gqa_fwd_split_launch: with fwd_split > 0 the heaviest query
+    blocks run as two key halves, and the work items are scheduled across
+    the XCDs dynamically (workspace and counters are the stream's cached
     buffers)."""
     lib = _lib.load()
     batch, num_heads, seq_q, head_dim = q.shape
@@ -251,14 +252,13 @@ def single_pass_forward(q, k, v, o, causal, fwd_split=0, return_lse=False):
     qkvo = (q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k),
             v.data_ptr(), _lib.strides(v), o.data_ptr(), _lib.strides(o))
     lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
+    # The stream's zeroed counters: split blocks' merge counters and the
+    # dynamic schedule's queues (both left zero by the kernel).
+    cnt = _counter_buffer(q.device, stream, lib.gqa_fwd_split_counters_count(batch, num_kv_heads, fwd_split))
+    ws = None
     if fwd_split > 0:
         ws = _workspace_buffer(q.device, stream,
                                lib.gqa_fwd_split_workspace_bytes(batch, num_kv_heads, head_dim, fwd_split))
-        cnt = _counter_buffer(q.device, stream, lib.gqa_fwd_split_counters_count(batch, num_kv_heads, fwd_split))
-        _lib.check(lib.gqa_fwd_split_launch(*qkvo, None if lse is None else lse.data_ptr(), ws.data_ptr(),
-                                            cnt.data_ptr(), fwd_split, *common))
-    elif lse is None:
-        _lib.check(lib.gqa_fwd_launch(*qkvo, *common))
-    else:
-        _lib.check(lib.gqa_fwd_lse_launch(*qkvo, lse.data_ptr(), *common))
+    _lib.check(lib.gqa_fwd_split_launch(*qkvo, None if lse is None else lse.data_ptr(),
+                                        None if ws is None else ws.data_ptr(), cnt.data_ptr(), fwd_split, *common))
     return o if lse is None else (o, lse)

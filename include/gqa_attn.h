@@ -102,8 +102,9 @@ int gqa_fwd_lse_launch(const void* q, const int64_t q_stride[4],
                        int seq_q, int seq_kv, int head_dim,
                        float scale_log2, int causal, int dtype, void* stream);
 
-/* Single pass with a key-range split of the heaviest query blocks (no
- * counterpart in the reference; its dispatch.py:35-45 only splits decode).
+/* Single pass with a key-range split of the heaviest query blocks and a
+ * dynamic schedule of its work items (no counterpart in the reference; its
+ * dispatch.py:35-45 only splits decode).
  * Under causal masking the query blocks of one (batch, kv head) carry from 1
  * to seq_kv/64 key tiles, so when there are few blocks per compute unit
  * (prefill at 2K tokens: 256 blocks for 256 CUs) the longest block sets the
@@ -113,10 +114,18 @@ int gqa_fwd_lse_launch(const void* q, const int64_t q_stride[4],
  * fp32 partial state (log-sum-exp merge) and writes o (and lse).  Results
  * equal gqa_fwd_launch's up to float rounding.  n_split in [0, number of
  * query blocks = ceil(seq_q / (256 / (num_heads / num_kv_heads)))];
- * workspace: gqa_fwd_split_workspace_bytes() bytes, 16-byte aligned;
- * counters: gqa_fwd_split_counters_count() int32, zero on the first call and
- * left zero by every call (one buffer serves all calls on one stream).  lse
- * may be NULL (no side output) or as in gqa_fwd_lse_launch. */
+ * workspace: gqa_fwd_split_workspace_bytes() bytes, 16-byte aligned (NULL
+ * allowed when n_split = 0); counters: gqa_fwd_split_counters_count() int32,
+ * zero on the first call and left zero by every call (one buffer serves all
+ * calls on one stream; calls that overlap must not share one).  With
+ * counters, the persistent single pass (head_dim 128, contiguous K/V) hands
+ * out its work items dynamically when there are at least 8 per compute
+ * unit: after a first static item, each workgroup takes the next from its
+ * XCD's queue and then from the other XCDs' — the XCDs run at different
+ * speeds under sustained MFMA load.
+ * counters may be NULL when n_split = 0 (static schedule, as
+ * gqa_fwd_launch).  The outputs do not depend on the schedule.  lse may be
+ * NULL (no side output) or as in gqa_fwd_lse_launch. */
 size_t gqa_fwd_split_workspace_bytes(int batch, int num_kv_heads, int head_dim, int n_split);
 size_t gqa_fwd_split_counters_count(int batch, int num_kv_heads, int n_split);
 int gqa_fwd_split_launch(const void* q, const int64_t q_stride[4],

@@ -212,8 +212,10 @@ def test_fwd_split_launch_validation(lib):
     assert lib.gqa_fwd_split_workspace_bytes(2, 8, 128, 5) == 2 * 8 * 5 * 2 * 512 * (64 + 2) * 4
     assert lib.gqa_fwd_split_workspace_bytes(1, 8, 64, 3) == 8 * 3 * 2 * 512 * (32 + 2) * 4
     assert lib.gqa_fwd_split_workspace_bytes(1, 8, 96, 3) == 0
-    assert lib.gqa_fwd_split_counters_count(2, 8, 5) == 80
-    assert lib.gqa_fwd_split_counters_count(2, 8, 0) == 0
+    # split blocks' counters, then the 32 scheduling counters
+    assert lib.gqa_fwd_split_counters_count(2, 8, 5) == 80 + 32
+    assert lib.gqa_fwd_split_counters_count(2, 8, 0) == 32
+    assert lib.gqa_fwd_split_counters_count(2, 8, -1) == 0
 
 
 def test_route_properties():
