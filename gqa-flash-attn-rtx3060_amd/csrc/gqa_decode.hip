@@ -199,9 +199,17 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
 
 }  // namespace
 
-template <int DT>
+// KV: 0 contiguous K/V; 1 a paged cache with pages of >= 64 keys (one
+// buffer descriptor per 64-key tile, from the block table); 2 pages of 4-32
+// keys (one descriptor per LDS-DMA instruction, whose 4 rows lie in one
+// page).  Paged caches are (num_blocks, block_size, Hkv, D) in any strides
+// (SplitParams::k/v: sb = block, ss = slot, sh = head stride); sequence b has
+// min(seq_lens[b], Skv) keys.  With q_start / q_len set, q is token-major and
+// sequence b has q_len[b] query rows from token q_start[b].
+template <int DT, int KV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_decode_kernel(SplitParams p) {
   constexpr int D = kDecD;
+  constexpr bool PAGED = KV != 0;
   using E = Elem<DT>;
   using T = typename E::T;
   using ST = FwdStage<D>;
@@ -232,7 +240,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   rest /= p.n_rblk;
   const int kvh = rest % dm.Hkv;
   const int b = rest / dm.Hkv;
-  const int skv = dm.Skv, sq = dm.Sq;
+  // Keys of this sequence (paged: its own length, clamped to [0, Skv], so no
+  // key past the block table's covered range is addressed) and its query
+  // rows (variable lengths: q_len[b] rows from token q_start[b]).
+  const int skv = PAGED ? min(max(load_uniform(p.seq_lens + b), 0), dm.Skv) : dm.Skv;
+  const bool varlen = p.q_len != nullptr;
+  const int sq = varlen ? min(max(load_uniform(p.q_len + b), 0), dm.Sq) : dm.Sq;
+  const int64_t tok0 = varlen ? (int64_t)load_uniform(p.q_start + b) : 0;
+  if ((32 * rb) / dm.G >= sq) return;  // a row block past this sequence's queries
 
   // This lane's query row (position-major packing).
   const int r = 32 * rb + i;
@@ -252,16 +267,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ntiles = (nk + 63) >> 6;
   const int qpos_lo = pos_lo + (skv - sq);
 
-  // Buffer descriptors over the chunk's K and V rows, each ending at the
-  // chunk's last key: rows of a partial last tile past it read as zero (and
-  // are masked).  The host bounds (chunk + 64) * row stride to 31 bits.
+  // Contiguous K/V: buffer descriptors over the chunk's K and V rows, each
+  // ending at the chunk's last key: rows of a partial last tile past it read
+  // as zero (and are masked).  The host bounds (chunk + 64) * row stride to
+  // 31 bits.  Paged: descriptors per tile or per instruction (issue).
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
   const char* kbase = static_cast<const char*>(p.k.ptr) +
-                      2 * ((int64_t)b * p.k.sb + (int64_t)kvh * p.k.sh + (int64_t)c0 * p.k.ss);
+                      2 * ((PAGED ? 0 : (int64_t)b * p.k.sb + (int64_t)c0 * p.k.ss) + (int64_t)kvh * p.k.sh);
   const char* vbase = static_cast<const char*>(p.v.ptr) +
-                      2 * ((int64_t)b * p.v.sb + (int64_t)kvh * p.v.sh + (int64_t)c0 * p.v.ss);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, nk > 0 ? (uint32_t)(nk - 1) * kssb + 2 * D : 0u);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, nk > 0 ? (uint32_t)(nk - 1) * vssb + 2 * D : 0u);
+                      2 * ((PAGED ? 0 : (int64_t)b * p.v.sb + (int64_t)c0 * p.v.ss) + (int64_t)kvh * p.v.sh);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, !PAGED && nk > 0 ? (uint32_t)(nk - 1) * kssb + 2 * D : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, !PAGED && nk > 0 ? (uint32_t)(nk - 1) * vssb + 2 * D : 0u);
+  const int* table_row = PAGED ? p.block_table + (int64_t)b * p.table_stride : nullptr;
 
   // Tile order.  With one head's keys in consecutive rows, every workgroup
   // would otherwise stream its chunk from the same relative offset in lock
@@ -286,9 +303,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // The prologue issues tiles 0 and 1 unconditionally (a tile past the
   // chunk reads zeros); the loop issues a tile only if it exists.
   auto issue = [&](int it, char* kst, char* vst) {
-    const uint32_t j = (uint32_t)tile_rel(it) * 64u;
-    issue_tile_dma<D, kDmaStream>(kst, rk, j * kssb, kssb, koff, wave);
-    issue_tile_dma<D, kDmaStream>(vst, rv, j * vssb, vssb, voff, wave);
+    const int j = tile_rel(it) * 64;
+    if constexpr (KV == 0) {
+      issue_tile_dma<D, kDmaStream>(kst, rk, (uint32_t)j * kssb, kssb, koff, wave);
+      issue_tile_dma<D, kDmaStream>(vst, rv, (uint32_t)j * vssb, vssb, voff, wave);
+    } else if constexpr (KV == 1) {
+      // The tile's 64 rows are one strided run inside one page; its
+      // descriptors start at the tile's first row and end at the chunk's
+      // last key (a tile past the chunk reads no table entry: zeros).
+      const int key0 = c0 + j, rows = c1 - key0;
+      __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
+      if (rows > 0) {
+        const int64_t pg = load_uniform(table_row + (key0 >> p.block_shift));
+        const int64_t slot = key0 & ((1 << p.block_shift) - 1);
+        const uint32_t n = (uint32_t)(min(rows, 64) - 1);
+        tk = make_rsrc(kbase + 2 * (pg * p.k.sb + slot * p.k.ss), n * kssb + 2 * D);
+        tv = make_rsrc(vbase + 2 * (pg * p.v.sb + slot * p.v.ss), n * vssb + 2 * D);
+      }
+      issue_tile_dma<D, kDmaStream>(kst, tk, 0u, kssb, koff, wave);
+      issue_tile_dma<D, kDmaStream>(vst, tv, 0u, vssb, voff, wave);
+    } else {
+      // Pages of 4-32 keys: instruction `step` loads rows [key, key + 4) of
+      // the tile, one run in one page; each gets its own descriptors.
+      typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+      for (int jj = 0; jj < NI; ++jj) {
+        const int step = jj * 4 + wave;
+        const int key = c0 + j + step * ST::RPI, rows = c1 - key;
+        __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
+        if (rows > 0) {
+          const int64_t pg = load_uniform(table_row + (key >> p.block_shift));
+          const int64_t slot = key & ((1 << p.block_shift) - 1);
+          const uint32_t n = (uint32_t)(min(rows, ST::RPI) - 1);
+          tk = make_rsrc(kbase + 2 * (pg * p.k.sb + slot * p.k.ss), n * kssb + 2 * D);
+          tv = make_rsrc(vbase + 2 * (pg * p.v.sb + slot * p.v.ss), n * vssb + 2 * D);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tk, (lds_void*)(kst + step * 1024), 16, koff, 0, 0, kDmaStream);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tv, (lds_void*)(vst + step * 1024), 16, voff, 0, 0, kDmaStream);
+      }
+    }
   };
 
   // Loads in issue order: tile 0, Q, tile 1 (the wait for tile 0 and Q then
@@ -301,7 +354,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   issue(0, lds_a_k0, lds_b_v0);
   u32x4 qreg[NKS];
   {
-    const char* qg = static_cast<const char*>(p.q.ptr) + 2 * ((int64_t)b * p.q.sb + (int64_t)kvh * dm.G * p.q.sh);
+    const char* qg = static_cast<const char*>(p.q.ptr) +
+                     2 * ((varlen ? tok0 * p.q.ss : (int64_t)b * p.q.sb) + (int64_t)kvh * dm.G * p.q.sh);
     const uint32_t qext = (uint32_t)(2 * ((int64_t)(dm.G - 1) * p.q.sh + (int64_t)(sq - 1) * p.q.ss + D));
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(qg, qext);
     const uint32_t qo = valid ? (uint32_t)(2 * ((int64_t)g * p.q.sh + (int64_t)pos * p.q.ss) + 16 * hh) : 0x80000000u;
@@ -481,7 +535,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
 
-  if (p.counters == nullptr) return;
+  if (PAGED || p.counters == nullptr) return;
   // Fused combine: count this partial once its stores have completed; the
   // workgroup completing the count for this (b, kv head, row block) combines.
   __builtin_amdgcn_s_waitcnt(0);
@@ -499,10 +553,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 bool decode_kernel_fits(const SplitParams& p) {
-  if (p.dm.D != kDecD || p.block_table != nullptr || p.q_len != nullptr) return false;
-  // 32-bit descriptor offsets: a chunk (plus a tile) of K and V rows, and
-  // the whole accumulator workspace.
-  const int64_t span = (int64_t)p.chunk + 64;
+  if (p.dm.D != kDecD) return false;
+  const bool paged = p.block_table != nullptr;
+  // Paged: whole LDS-DMA instructions (4 rows at head_dim 128) in a page,
+  // and 64-key-aligned chunks (so a tile lies in a page of >= 64 keys).
+  if (paged && ((1 << p.block_shift) < FwdStage<kDecD>::RPI || (p.chunk & 63) != 0)) return false;
+  // 32-bit descriptor offsets: (contiguous) a chunk plus a tile of K and V
+  // rows, (paged) a tile of rows; the whole accumulator workspace.
+  const int64_t span = paged ? 64 : (int64_t)p.chunk + 64;
   if (span * p.k.ss * 2 >= ((int64_t)1 << 31) || span * p.v.ss * 2 >= ((int64_t)1 << 31)) return false;
   const int64_t acc_bytes = (int64_t)p.dm.B * p.dm.Hq * p.dm.Sq * p.splits * kDecD * 4;
   // ... and a kv head's query group (its G heads x Sq rows).
@@ -510,16 +568,22 @@ bool decode_kernel_fits(const SplitParams& p) {
   return acc_bytes <= 0xFFFFFFF0ll && q_bytes < ((int64_t)1 << 31);
 }
 
-template <int DT>
+template <int DT, int KV>
 static hipError_t launch_decode_t(const SplitParams& p, hipStream_t stream) {
   const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * p.n_rblk * p.splits;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_decode_kernel<DT>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gqa_decode_kernel<DT, KV>), dim3((unsigned)total), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
+template <int KV>
+static hipError_t launch_decode_kv(const SplitParams& p, int dtype, hipStream_t stream) {
+  return dtype == 0 ? launch_decode_t<0, KV>(p, stream) : launch_decode_t<1, KV>(p, stream);
+}
+
 hipError_t launch_decode_first(const SplitParams& p, int dtype, hipStream_t stream) {
-  return dtype == 0 ? launch_decode_t<0>(p, stream) : launch_decode_t<1>(p, stream);
+  if (p.block_table == nullptr) return launch_decode_kv<0>(p, dtype, stream);
+  return p.block_shift >= 6 ? launch_decode_kv<1>(p, dtype, stream) : launch_decode_kv<2>(p, dtype, stream);
 }
 
 }  // namespace gqa

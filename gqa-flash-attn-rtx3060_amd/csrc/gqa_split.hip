@@ -549,6 +549,7 @@ static hipError_t launch_paged_t(const SplitParams& p, int dtype, hipStream_t st
 
 // Requires p.chunk to be a multiple of 64 (sub-tiles start 64-aligned).
 hipError_t launch_paged_split_first(const SplitParams& p, int dtype, hipStream_t stream) {
+  if (decode_kernel_fits(p)) return launch_decode_first(p, dtype, stream);
   return p.block_shift >= 6 ? launch_paged_t<1>(p, dtype, stream) : launch_paged_t<2>(p, dtype, stream);
 }
 
