@@ -114,3 +114,46 @@ def test_split_results_do_not_depend_on_which_half_merges(n_split):
     ref = _run(q, k, v, True, n_split)
     for _ in range(24):
         assert torch.equal(_run(q, k, v, True, n_split), ref)
+
+
+def test_dynamic_schedule_equals_static_schedule():
+    # With at least 8 work items per compute unit the persistent single pass
+    # schedules its items dynamically across the XCDs when given counters
+    # (gqa_fwd_split_launch, the Python route); items are independent, so
+    # the outputs are bit-identical to the static schedule of gqa_fwd_launch,
+    # on every call, and the counters are left zero.
+    from gqa_kernels import _lib, gqa_split
+    from gqa_kernels.dispatch import LOG2E, _cu_count
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    items = B * Hkv * S // (256 // (Hq // Hkv))
+    assert items >= 8 * min(items, _cu_count(0)), "shape too small for the dynamic schedule"
+    q, k, v = make_inputs(B, Hq, Hkv, S, S, D, torch.bfloat16, seed=11, device=DEV)
+    lib = _lib.load()
+    o_static = torch.empty_like(q)
+    print(f"dynamic vs static schedule B={B} S={S} items={items}", flush=True)
+    _lib.check(lib.gqa_fwd_launch(q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k), v.data_ptr(),
+                                  _lib.strides(v), o_static.data_ptr(), _lib.strides(o_static), B, Hq, Hkv, S, S,
+                                  D, D ** -0.5 * LOG2E, 1, _lib.DTYPE_BF16,
+                                  torch.cuda.current_stream().cuda_stream))
+    outs = [_run(q, k, v, True, 0) for _ in range(4)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, o_static)
+    for buf in gqa_split._counters.values():
+        assert int(buf.abs().sum().item()) == 0
+    rows = _rows(S, 32)
+    ref = oracle(q[:1, :4], k[:1, :1], v[:1, :1], True, rows=rows)
+    assert_close(to_np(outs[0])[:1, :4][:, :, rows], ref, BASELINE_TOL[torch.bfloat16], "dynamic schedule")
+
+
+def test_dynamic_schedule_with_split_blocks_repeats_exactly():
+    # Split blocks under the dynamic schedule: either half may run on any
+    # XCD; repeated calls give the same bits, close to the unsplit result.
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    q, k, v = make_inputs(B, Hq, Hkv, S, S, D, torch.bfloat16, seed=12, device=DEV)
+    ref = _run(q, k, v, True, 4)
+    for _ in range(6):
+        assert torch.equal(_run(q, k, v, True, 4), ref)
+    o0 = _run(q, k, v, True, 0)
+    torch.cuda.synchronize()
+    assert errors(ref, o0)[0] <= 1.6e-2
