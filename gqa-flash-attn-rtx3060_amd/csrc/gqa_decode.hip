@@ -5,7 +5,7 @@
 // gqa_kernels/gqa_split.py:26-112) and, when fused, gqa_split_reduce_kernel
 // (gqa_split.py:115-147).  The work decomposition, the packed rows and the
 // partials are those of gqa_split.hip: one workgroup per (batch, kv head,
-// 32-row block, split), rows packed position-major (row r -> position r / G,
+// row block of 32 or 64 rows, split), rows packed position-major (row r -> position r / G,
 // head r % G), partials (m in log2 units, l, unnormalised acc) per (row,
 // split) in the same workspace layout.
 //
@@ -24,6 +24,12 @@
 // the chunk each wave stores its own 32 dims of the valid rows' partials —
 // no cross-wave merge.  With a decode group of 4 query rows most of each
 // S^T MFMA is padding; it runs hidden under the HBM stream.
+//
+// Wide row blocks (RW = 2, for 33-64 packed rows per kv head, e.g. verify
+// steps of 9-16 tokens at G = 4): one workgroup takes two 32-row blocks, so
+// the chunk's K/V stream once instead of once per 32-row block.  Waves 2h
+// and 2h + 1 take rows [32h, 32h + 32) of the block, each with 64 of the
+// 128 dims; partials and the fused combine stay per 32-row block.
 //
 // Fused combine (SplitParams::counters set): the last workgroup of each
 // (b, kv head, row block) to count its partial in combines all splits
@@ -206,7 +212,8 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
 // (SplitParams::k/v: sb = block, ss = slot, sh = head stride); sequence b has
 // min(seq_lens[b], Skv) keys.  With q_start / q_len set, q is token-major and
 // sequence b has q_len[b] query rows from token q_start[b].
-template <int DT, int KV>
+// RW: 32-row blocks per workgroup (1 or 2).
+template <int DT, int KV, int RW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_decode_kernel(SplitParams p) {
   constexpr int D = kDecD;
   constexpr bool PAGED = KV != 0;
@@ -229,17 +236,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const Dims& dm = p.dm;
   const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;  // also this wave's 32-dim block of O^T
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;
   const int i = lane & 31, hh = lane >> 5;
+  // This wave's 32-row half of the block (rh) and its NDB 32-dim blocks of
+  // O^T from db0: RW = 1, dim block `wave`; RW = 2, dim blocks 2 (wave & 1)
+  // and 2 (wave & 1) + 1.
+  constexpr int NDB = RW;
+  const int rh = RW == 2 ? wave >> 1 : 0;
+  const int db0 = RW == 2 ? 2 * (wave & 1) : wave;
 
-  const int total = dm.B * dm.Hkv * p.n_rblk * p.splits;
+  const int n_wblk = (p.n_rblk + RW - 1) / RW;
+  const int total = dm.B * dm.Hkv * n_wblk * p.splits;
   const int w = xcd_remap(blockIdx.x, total);
   const int s = w % p.splits;
   int rest = w / p.splits;
-  const int rb = rest % p.n_rblk;
-  rest /= p.n_rblk;
+  const int rbw = rest % n_wblk;
+  rest /= n_wblk;
   const int kvh = rest % dm.Hkv;
   const int b = rest / dm.Hkv;
+  const int rb = RW * rbw + rh;  // this wave's 32-row block
   // Keys of this sequence (paged: its own length, clamped to [0, Skv], so no
   // key past the block table's covered range is addressed) and its query
   // rows (variable lengths: q_len[b] rows from token q_start[b]).
@@ -247,7 +262,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool varlen = p.q_len != nullptr;
   const int sq = varlen ? min(max(load_uniform(p.q_len + b), 0), dm.Sq) : dm.Sq;
   const int64_t tok0 = varlen ? (int64_t)load_uniform(p.q_start + b) : 0;
-  if ((32 * rb) / dm.G >= sq) return;  // a row block past this sequence's queries
+  const int wr0 = 32 * RW * rbw;        // the workgroup's first packed row
+  if (wr0 / dm.G >= sq) return;          // a row block past this sequence's queries
 
   // This lane's query row (position-major packing).
   const int r = 32 * rb + i;
@@ -260,8 +276,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // visible key under causal.
   const int c0 = s * p.chunk;
   int c1 = min(c0 + p.chunk, skv);
-  const int pos_lo = (32 * rb) / dm.G;
-  const int pos_hi = min(sq - 1, (32 * rb + 31) / dm.G);
+  const int pos_lo = wr0 / dm.G;
+  const int pos_hi = min(sq - 1, (wr0 + 32 * RW - 1) / dm.G);
   if (dm.causal) c1 = min(c1, pos_hi + (skv - sq) + 1);
   const int nk = max(c1 - c0, 0);
   const int ntiles = (nk + 63) >> 6;
@@ -377,15 +393,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
     ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
-  uint32_t vb;
+  uint32_t vb[NDB];
   {
     const int q = lane >> 4, ii = lane & 15;
     const int rowl = 8 * (q >> 1) + (ii >> 2);
     const int f = ii >> 2;  // sv(rowl) / 4
-    vb = (uint32_t)(rowl * (2 * D) + 16 * (4 * (wave ^ f) + 2 * (q & 1) + ((ii & 3) >> 1)) + 8 * (ii & 1)) & kVMask;
+#pragma unroll
+    for (int d = 0; d < NDB; ++d)
+      vb[d] = (uint32_t)(rowl * (2 * D) + 16 * (4 * ((db0 + d) ^ f) + 2 * (q & 1) + ((ii & 3) >> 1)) + 8 * (ii & 1)) &
+              kVMask;
   }
 
-  f32x16 acc = {};
+  f32x16 acc[NDB] = {};
   float m_run = -__builtin_inff(), l_run = 0.f;
   const float c = dm.c;
 
@@ -478,17 +497,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     l_run = l_run * alpha + rs;
     m_run = m_new;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] *= alpha;
-
-    // O^T (this wave's 32 dims) += V^T P^T over the 64 keys.
+    for (int d = 0; d < NDB; ++d)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int mb = j >> 1, kk = j & 1;
-      const int ro = (32 * mb + 16 * kk) * (2 * D);
-      const u32x2 lo = ld_tr(cv + vb + ro);
-      const u32x2 hi = ld_tr(cv + vb + ro + 4 * (2 * D));
-      acc = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[mb][kk], acc);
-    }
+      for (int v = 0; v < 16; ++v) acc[d][v] *= alpha;
+
+    // O^T (this wave's dims) += V^T P^T over the 64 keys.
+#pragma unroll
+    for (int d = 0; d < NDB; ++d)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int mb = j >> 1, kk = j & 1;
+        const int ro = (32 * mb + 16 * kk) * (2 * D);
+        const u32x2 lo = ld_tr(cv + vb[d] + ro);
+        const u32x2 hi = ld_tr(cv + vb[d] + ro + 4 * (2 * D));
+        acc[d] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[mb][kk], acc[d]);
+      }
     // Every wave is done with this stage: refill it with the tile two ahead.
     phase_barrier();
     if constexpr (ISSUE) issue(it + 2, kst, vst);
@@ -516,20 +539,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // stages.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // This wave's 32 dims of the valid rows' partials: lane (i, hh) holds
-  // dims 32 * wave + 8 * j + 4 * hh + 0..3 in acc[4j .. 4j + 3].
+  // This wave's dims of the valid rows' partials: lane (i, hh) holds dims
+  // 32 * (db0 + d) + 8 * j + 4 * hh + 0..3 in acc[d][4j .. 4j + 3].
   const float l_tot = xhalf_sum(l_run);
   if (valid) {
     const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
-    const uint32_t ob = (uint32_t)((row * D + 32 * wave + 4 * hh) * 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      store_coherent4(rw, ob + 32u * j, f32x4{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]});
+    for (int d = 0; d < NDB; ++d) {
+      const uint32_t ob = (uint32_t)((row * D + 32 * (db0 + d) + 4 * hh) * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        store_coherent4(rw, ob + 32u * j,
+                        f32x4{acc[d][4 * j], acc[d][4 * j + 1], acc[d][4 * j + 2], acc[d][4 * j + 3]});
+    }
     // A sequence without keys stores m = 0, l = 0 (never produced otherwise:
     // the chunk's largest score contributes exp2(0) = 1 to l), which the
-    // combine turns into a zero row.
-    if (wave == 0 && hh == 0) {
+    // combine turns into a zero row.  One wave per row half stores them.
+    if (db0 == 0 && hh == 0) {
       store_coherent(p.ws_m + row, skv == 0 ? 0.f : m_run * c);
       store_coherent(p.ws_l + row, l_tot);
     }
@@ -537,11 +564,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   if (PAGED || p.counters == nullptr) return;
   // Fused combine: count this partial once its stores have completed; the
-  // workgroup completing the count for this (b, kv head, row block) combines.
+  // workgroup completing the count for this (b, kv head, row block) combines
+  // (a wide block counts on its first 32-row block's counter and combines
+  // both).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (t == 0) {
-    const int idx = (b * dm.Hkv + kvh) * p.n_rblk + rb;
+    const int idx = (b * dm.Hkv + kvh) * p.n_rblk + RW * rbw;
     const int prev = __hip_atomic_fetch_add(&p.counters[idx], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == p.splits - 1);
     // Every increment of this call has landed: leave the counter zero.
@@ -549,7 +578,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   __syncthreads();
   if (!s_last) return;
-  decode_combine<DT>(p, b, kvh, rb, t, lds_a_k0);
+  // One call site in a loop (a second inlined copy of the combine would
+  // put its register arrays on the stack).
+#pragma unroll 1
+  for (int rbc = RW * rbw; rbc < RW * rbw + RW && rbc < p.n_rblk && (32 * rbc) / dm.G < sq; ++rbc) {
+    if (rbc > RW * rbw) __syncthreads();  // the previous combine's LDS reads are done
+    decode_combine<DT>(p, b, kvh, rbc, t, lds_a_k0);
+  }
 }
 
 bool decode_kernel_fits(const SplitParams& p) {
@@ -568,11 +603,17 @@ bool decode_kernel_fits(const SplitParams& p) {
   return acc_bytes <= 0xFFFFFFF0ll && q_bytes < ((int64_t)1 << 31);
 }
 
+// Two 32-row blocks per workgroup whenever a kv head has more than one
+// (each K/V chunk is then streamed once per 64 rows, not per 32).
 template <int DT, int KV>
 static hipError_t launch_decode_t(const SplitParams& p, hipStream_t stream) {
-  const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * p.n_rblk * p.splits;
+  const int rw = p.n_rblk >= 2 ? 2 : 1;
+  const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * ((p.n_rblk + rw - 1) / rw) * p.splits;
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gqa_decode_kernel<DT, KV>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  if (rw == 2)
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 2>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 1>), dim3((unsigned)total), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -25,6 +25,9 @@ LOG2E = math.log2(math.e)
 # Packed query rows of one single-pass workgroup, and of one split-KV row block.
 FWD_ROWS = 256
 SPLIT_ROWS = 32
+# At head_dim 128 one split-KV workgroup takes two row blocks when a kv head
+# has more than one (each K/V chunk is then streamed once per 64 rows).
+SPLIT_WIDE_ROWS = 64
 # The split-KV path is taken for at most this many packed rows per kv head.
 SPLIT_MAX_ROWS = 64
 # Shortest key cache worth splitting (the reference's threshold, dispatch.py:37).
@@ -126,8 +129,14 @@ def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
     return best_ns if best <= (1.0 - FWD_SPLIT_GAIN) * base else 0
 
 
+def split_rows_per_workgroup(rows: int, head_dim: int = 128) -> int:
+    """Packed rows one split-KV workgroup covers (the first pass's row
+    blocks: 32, or two of them at head_dim 128)."""
+    return SPLIT_WIDE_ROWS if head_dim == 128 and rows > SPLIT_ROWS else SPLIT_ROWS
+
+
 def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
-                 cu_count: int, causal: bool = True) -> Route:
+                 cu_count: int, causal: bool = True, head_dim: int = 128) -> Route:
     """Pick the kernel path for one call (pure function of the shapes).
 
     Counterpart of reference dispatch.py:35-45.  A query block of at most
@@ -142,7 +151,7 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     rows = group * seq_q
     single_wgs = _cdiv(seq_q, max(1, FWD_ROWS // group)) * num_kv_heads * batch
     if rows <= SPLIT_MAX_ROWS and seq_kv >= SPLIT_MIN_KV:
-        base = _cdiv(rows, SPLIT_ROWS) * num_kv_heads * batch
+        base = _cdiv(rows, split_rows_per_workgroup(rows, head_dim)) * num_kv_heads * batch
         target = SPLIT_WG_PER_CU * cu_count
         splits = 1
         while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
@@ -211,7 +220,7 @@ def gqa_flash_attn(q, k, v, causal=True, *, return_lse=False):
     dev = q.get_device()  # device index (an int: no torch.device objects on this path)
     assert k.get_device() == dev and v.get_device() == dev, "q, k, v must be on one device"
 
-    route = _route_cached(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev), bool(causal))
+    route = _route_cached(batch, num_heads, num_kv_heads, seq_q, seq_kv, _cu_count(dev), bool(causal), head_dim)
     if dev == torch.cuda.current_device():
         return _launch(route, q, k, v, causal, return_lse, dev)
     with torch.cuda.device(dev):  # launch on q's device

@@ -84,14 +84,18 @@ def paged_chunk(max_seq_len: int, splits: int) -> int:
 
 
 def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
-                 cu_count: int, block_size: int = 64) -> int:
+                 cu_count: int, block_size: int = 64, head_dim: int = 128) -> int:
     """Split count for a paged call: the power of two that brings the first
     pass to two workgroups per compute unit while every chunk keeps at least
     256 keys (pure function of the shapes).  With pages under 64 keys a chunk
     spans at most GQA_PAGED_CHUNK_PAGES pages (the slice of the block table a
     workgroup stages in LDS), which can ask for more splits."""
     group = num_heads // num_kv_heads
-    base = -(-group * seq_q // _SPLIT_ROWS) * num_kv_heads * batch
+    rows = group * seq_q
+    # Rows per first-pass workgroup: two 32-row blocks at head_dim 128 with
+    # pages of >= 4 keys (the LDS-DMA first pass), else one.
+    wide = head_dim == 128 and block_size >= 4 and rows > _SPLIT_ROWS
+    base = -(-rows // (2 * _SPLIT_ROWS if wide else _SPLIT_ROWS)) * num_kv_heads * batch
     target = _SPLIT_WG_PER_CU * cu_count
     splits = 1
     while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
@@ -225,7 +229,8 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     assert 0 <= max_seq_len <= capacity, "max_seq_len exceeds the block table's capacity"
     dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
     if splits is None:
-        splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), block_size)
+        splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), block_size,
+                              head_dim)
     if scale is None:
         scale = head_dim ** -0.5
 

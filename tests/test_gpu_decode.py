@@ -49,3 +49,49 @@ def test_decode_g8_rows_fill_a_block():
     o = gqa_flash_attn(q, k, v, causal=True)
     torch.cuda.synchronize()
     assert_close(o, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], "G = 8, Sq = 4")
+
+
+@pytest.mark.parametrize("Hq,Hkv,sq,skv,S", [
+    (32, 8, 9, 3 * 64 * 5 + 11, 4),   # 36 rows: the second 32-row block holds 4
+    (32, 8, 16, 4096, 8),             # 64 rows: both blocks full
+    (12, 4, 15, 2000, 3),             # G = 3: position 10 straddles the two blocks
+    (64, 8, 5, 1000, 2),              # G = 8: 40 rows
+    (32, 8, 12, 256, 8),              # 32-key chunks: the causal diagonal crosses chunks
+    (32, 8, 16, 10, 2),               # seq_q > seq_kv: rows of positions 0-5 see no key (NaN)
+])
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_wide_row_blocks(Hq, Hkv, sq, skv, S, fused):
+    # 33-64 packed rows per kv head: one workgroup covers two 32-row blocks
+    # (waves 0-1 the first, 2-3 the second), streaming each chunk once; the
+    # partials and the combine stay per 32-row block.
+    from gqa_kernels.gqa_split import split_kv_forward
+    from oracle.gqa_oracle import gqa_lse
+    q, k, v = make_inputs(1, Hq, Hkv, sq, skv, 128, torch.bfloat16, seed=sq * skv + S, device=DEV)
+    print(f"wide row blocks Hq={Hq} Hkv={Hkv} sq={sq} skv={skv} S={S} fused={fused}", flush=True)
+    o, lse = split_kv_forward(q, k, v, True, S, fused=fused, return_lse=True)
+    torch.cuda.synchronize()
+    ref = oracle(q, k, v)
+    got = to_np(o)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan), "fully masked rows differ"
+    assert_close(got[~nan], ref[~nan], BASELINE_TOL[torch.bfloat16], f"sq={sq} skv={skv} S={S}")
+    ref_l = gqa_lse(to_np(q), to_np(k), to_np(v), True)
+    fin = np.isfinite(ref_l)
+    got_l = to_np(lse)
+    assert np.array_equal(np.isneginf(got_l), ~fin)
+    assert np.abs(got_l[fin] - ref_l[fin]).max() <= 2e-3
+
+
+def test_decode_wide_row_blocks_route_and_repeatability():
+    # A 16-token verify step at G = 4 through the public entry point (split
+    # route, 64-row workgroups): oracle parity, and the same bits on every
+    # call (fixed combine order).
+    from gqa_kernels import gqa_flash_attn
+    from gqa_kernels.dispatch import _cu_count, choose_route
+    assert choose_route(2, 32, 8, 16, 20000, _cu_count(0)).kind == "split"
+    q, k, v = make_inputs(2, 32, 8, 16, 20000, 128, torch.bfloat16, seed=16, device=DEV)
+    o = gqa_flash_attn(q, k, v, causal=True)
+    for _ in range(3):
+        assert torch.equal(gqa_flash_attn(q, k, v, causal=True), o)
+    torch.cuda.synchronize()
+    assert_close(o, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], "verify step")

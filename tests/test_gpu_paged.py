@@ -79,6 +79,8 @@ def _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype):
     (2, 32, 4, 16, [1500, 260], 64, 256, torch.bfloat16, False),          # chunk, non-causal, big pages
     (1, 16, 16, 1, [333], 128, 1, torch.bfloat16, True),                  # MHA, one-slot pages
     (3, 32, 8, 1, [0, 500, 64], 128, 16, torch.bfloat16, True),           # a sequence without keys: zeros
+    (2, 32, 8, 16, [3000, 700], 128, 16, torch.bfloat16, True),           # 64 rows: one wide row block
+    (3, 32, 8, 9, [1300, 64, 5], 128, 64, torch.float16, True),           # 36 rows, a sequence shorter than Sq
 ])
 def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal):
     from gqa_kernels.paged import paged_attention

@@ -177,6 +177,27 @@ def test_route_baseline_configs():
     assert choose_route(1, 32, 8, 1, 512, cu).kind == "single"
 
 
+def test_route_wide_row_blocks():
+    # 33-64 packed rows per kv head (verify steps of 9-16 tokens at G = 4):
+    # at head_dim 128 one workgroup covers both 32-row blocks, so the split
+    # count is sized for half as many workgroups per split as at head_dim 64.
+    from gqa_kernels.dispatch import choose_route, split_rows_per_workgroup
+    from gqa_kernels.paged import paged_splits
+    cu = 256
+    assert split_rows_per_workgroup(32) == 32 and split_rows_per_workgroup(33) == 64
+    assert split_rows_per_workgroup(64, 64) == 32
+    for sq in (9, 16):
+        r = choose_route(1, 32, 8, sq, 131072, cu)
+        assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
+        r64 = choose_route(1, 32, 8, sq, 131072, cu, True, 64)
+        assert r64.kind == "split" and r64.splits == 32 and r64.workgroups == 512
+    assert choose_route(1, 32, 8, 8, 131072, cu).workgroups == 512
+    assert choose_route(1, 32, 8, 17, 131072, cu).kind == "single"
+    assert paged_splits(1, 32, 8, 16, 131072, cu) == 64
+    assert paged_splits(1, 32, 8, 16, 131072, cu, block_size=16) == 64
+    assert paged_splits(1, 32, 8, 16, 131072, cu, head_dim=64) == 32
+
+
 def test_fwd_split_choice():
     from gqa_kernels.dispatch import _fwd_block_tiles, choose_fwd_split, choose_route, fwd_split_makespan
     cu = 256
