@@ -25,7 +25,8 @@ using gqa::TensorRef;
 // 10: gqa_fwd_split_counters_count adds the persistent single pass's
 // scheduling counters (also for n_split = 0); gqa_fwd_split_launch with
 // counters schedules the work items across the XCDs dynamically.
-constexpr int kAbiVersion = 10;
+// 11: gqa_fwd_chunks_launch (single pass over key chunks + split combine).
+constexpr int kAbiVersion = 11;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -489,6 +490,47 @@ int gqa_split_reduce_lse_launch(const float* workspace, int splits, void* o, con
   const int rc = check_lse(lse);
   if (rc && batch > 0 && seq_q > 0) return rc;
   return reduce_impl(workspace, splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream);
+}
+
+int gqa_fwd_chunks_launch(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                          const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4], float* lse,
+                          float* workspace, int* counters, int kv_splits, int batch, int num_heads,
+                          int num_kv_heads, int seq_q, int seq_kv, int head_dim, float scale_log2, int causal,
+                          int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, dtype);
+  if (rc) return rc;
+  const int G = num_heads / num_kv_heads;
+  if (G > gqa::kFwdRows) return GQA_E_GROUP;
+  if (kv_splits < 1 || kv_splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (workspace == nullptr) return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || (reinterpret_cast<uintptr_t>(counters) & 3u) != 0)
+    return GQA_E_STRIDE;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
+  if (seq_kv > 0 && ((rc = check_tensor(k, k_stride)) || (rc = check_tensor(v, v_stride)))) return rc;
+  if (seq_kv > 0 && (!rows_fit_32bit(seq_kv, k_stride) || !rows_fit_32bit(seq_kv, v_stride))) return GQA_E_STRIDE;
+
+  gqa::FwdParams p{};
+  p.q = ref(q, q_stride);
+  p.k = ref(k, k_stride);
+  p.v = ref(v, v_stride);
+  p.o = ref(o, o_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, G, scale_log2, causal ? 1 : 0};
+  p.block_m = gqa::kFwdRows / G;
+  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  p.lse = nullptr;  // written by the combine
+  p.sched = counters;
+  const int tiles = (seq_kv + gqa::kFwdTileKeys - 1) / gqa::kFwdTileKeys;
+  p.kv_splits = kv_splits;
+  p.kv_chunk_tiles = std::max((tiles + kv_splits - 1) / kv_splits, 1);
+  const size_t rows = (size_t)batch * num_heads * seq_q * kv_splits;
+  p.ws_acc = workspace;
+  p.ws_m = workspace + rows * head_dim;
+  p.ws_l = p.ws_m + rows;
+  rc = to_code(gqa::launch_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+  if (rc) return rc;
+  return reduce_impl(workspace, kv_splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream);
 }
 
 int gqa_split_reduce_varlen_launch(const float* workspace, int splits, void* o, const int64_t o_stride[4],

@@ -146,7 +146,9 @@ __device__ __forceinline__ void mphase_pipe() {
 // next item's first K/V tiles and Q, and the output stores drain while
 // those loads are in flight.  The workgroup launch between items leaves the
 // critical path.
-template <int DT, int D, int PG>
+// KC: key chunks (FwdParams::kv_splits > 0; contiguous K/V only), a
+// separate instance so the others keep their registers.
+template <int DT, int D, int PG, bool KC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void gqa_fwd_kernel(
     FwdParams p) {
   using E = Elem<DT>;
@@ -191,7 +193,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // split, the n_split heaviest blocks of each (b, kv head) come as two
   // items: first the upper halves of their key ranges, then (in the usual
   // order) the lower halves and the unsplit blocks.
-  const int n_items = p.n_mblk + p.n_split;
+  // Key chunks (contiguous K/V only): kv_splits items per query block, the
+  // blocks of one chunk consecutive (they read the same keys).
+  constexpr bool chunked = KC && PG == 0;
+  const int n_items = chunked ? p.n_mblk * p.kv_splits : p.n_mblk + p.n_split;
   const int total = n_items * dm.Hkv * dm.B;
   // The k-th item of this workgroup (-1: none).  One item per workgroup
   // (xcd_remap), or persistent: the workgroups of XCD x (hardware ids x,
@@ -249,7 +254,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   auto decode = [&](int w, int i, int block_m) __attribute__((always_inline)) -> Item {
     Item x;
     x.bh = w / n_items;
-    const int idx = w - x.bh * n_items;
+    int idx = w - x.bh * n_items;
+    int chunk = 0;
+    if constexpr (chunked) {
+      chunk = idx / p.n_mblk;
+      idx -= chunk * p.n_mblk;
+    }
     if (idx < p.n_split) {
       x.pid_m = p.n_mblk - 1 - idx;
       x.part = 1;
@@ -282,6 +292,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     const int tsplit = ntiles_all >> 1;
     x.tb = (x.part == 1) ? tsplit : 0;
     x.ntiles = (x.part == 0) ? tsplit : ntiles_all - x.tb;
+    if constexpr (chunked) {
+      // Tiles [chunk * ct, (chunk + 1) * ct) of the block's range (none
+      // for a chunk past it: an empty partial).
+      x.tb = chunk * p.kv_chunk_tiles;
+      x.ntiles = max(min(ntiles_all - x.tb, p.kv_chunk_tiles), 0);
+    }
     x.qpos_lo = pos_lo + (x.skv - x.sq);
     // Global side: buffer descriptors over this (b, kv head)'s K and V rows,
     // each ending at the last byte of row seq_kv - 1.  The host guarantees
@@ -666,7 +682,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     // increment finds 1 merges.  Every increment follows its item's completed
     // stores, so a counter of 1 means the other state is readable.
     bool write_out = true;
-    if (ie.part >= 0) {
+    if (!chunked && ie.part >= 0) {
       constexpr int PF_ = kFwdPartFloats(D);
       constexpr int NA = NDB * 16;  // accumulators per lane
       const int slot = ie.bh * p.n_split + (p.n_mblk - 1 - ie.pid_m);
@@ -718,7 +734,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       write_out = last;
     }
 
-    if (write_out) {
+    if constexpr (chunked) {
+      // Key chunk: the partial state of this lane's row, as the split-KV
+      // first pass stores it (m = m_ref * c in log2 units, relative to which
+      // l and acc are kept; -inf with l = 0 for a row that saw no key in
+      // this chunk; 0 for a sequence without keys, which the combine turns
+      // into a zero row).  Lane (i, hh) holds dims 32 db + 8 j + 4 hh + 0..3
+      // of its row in acc[db][4 j .. 4 j + 3].
+      const float l_tot = xhalf_sum(l_run);
+      if (ie.valid) {
+        const int chunk = ie.tb / p.kv_chunk_tiles;
+        const int64_t row = (((int64_t)ie.b * dm.Hq + ie.head) * dm.Sq + ie.pos) * p.kv_splits + chunk;
+        float* wa = p.ws_acc + row * D + 4 * hh_e;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4*>(wa + 32 * db + 8 * j) =
+                f32x4{acc[db][4 * j], acc[db][4 * j + 1], acc[db][4 * j + 2], acc[db][4 * j + 3]};
+        if (hh_e == 0) {
+          p.ws_m[row] = ie.skv == 0 ? 0.f : m_run * c;
+          p.ws_l[row] = l_tot;
+        }
+      }
+    } else if (write_out) {
       // Epilogue: o = acc / l (0/0 = NaN for a row whose keys are all
       // masked, as the reference's acc / l_i at gqa_fwd.py:106).  A sequence
       // with no keys at all gives zero rows instead: tests/reference.py:33-34
@@ -845,7 +884,8 @@ static int device_cu_count() {
 
 template <int DT, int D, int PG>
 static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
-  const int total = (p.n_mblk + p.n_split) * p.dm.Hkv * p.dm.B;
+  const int per_bh = (PG == 0 && p.kv_splits > 0) ? p.n_mblk * p.kv_splits : p.n_mblk + p.n_split;
+  const int total = per_bh * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
   int grid = total;
   if (PG == 0 && D == 128) {
@@ -861,7 +901,10 @@ static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
   } else {
     p.sched = nullptr;
   }
-  hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
+  if (PG == 0 && p.kv_splits > 0)
+    hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, 0, true>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -53,6 +53,17 @@ struct FwdParams {
   // Persistent single pass: nullptr (static schedule) or kFwdSchedCounters
   // zero-initialised ints (dynamic schedule across XCDs), left zero.
   int* sched;
+  // Key chunks (contiguous K/V, fixed query lengths; n_split = 0): when
+  // kv_splits > 0 every query block runs as kv_splits work items over
+  // consecutive ranges of kv_chunk_tiles key tiles, each writing the fp32
+  // partial (m in log2 units, l, unnormalised acc) of its valid rows into
+  // the split-KV workspace layout (SplitParams::ws_*; the split combine
+  // then writes o and lse) instead of o.
+  int kv_splits;
+  int kv_chunk_tiles;
+  float* ws_acc;  // (B, Hq, Sq, kv_splits, D)
+  float* ws_m;    // (B, Hq, Sq, kv_splits)
+  float* ws_l;    // (B, Hq, Sq, kv_splits)
 };
 
 // Split-KV first pass: one workgroup per (b, kv head, row block, split).

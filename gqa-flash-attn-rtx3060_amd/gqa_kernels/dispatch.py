@@ -52,13 +52,23 @@ FWD_SPLIT_GAIN = 0.05
 # measured: 8 of 16 blocks, -18 %; 8 of 32, -10 %; none at 4096).
 FWD_ITEM_OVERHEAD = 8
 FWD_TILE = 64
+# Key chunks (single pass over kv_splits key ranges per query block, then
+# the split-KV combine): considered when there are fewer query blocks than
+# compute units.  Per-item overhead (first loads, partial store) in tile
+# steps; a tile step of the single pass takes ~1.65 us on MI355X, the
+# combine launch ~3 us plus its read of the fp32 partials at ~5 TB/s.
+CHUNK_ITEM_OVERHEAD = 8
+CHUNK_MIN_TILES = 4
+TILE_STEP_US = 1.65
+COMBINE_LAUNCH_US = 3.0
+COMBINE_BYTES_PER_US = 5.0e6
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 
 
 @dataclass(frozen=True)
 class Route:
-    kind: str  # "single" or "split"
+    kind: str  # "single", "split" or "chunks" (splits: key chunks per query block)
     splits: int = 1
     workgroups: int = 0
     fwd_split: int = 0  # single pass: query blocks per (b, kv head) run as two key halves
@@ -105,6 +115,68 @@ def fwd_split_makespan(tiles, n_split: int, n_bh: int, cu_count: int, causal: bo
     return worst
 
 
+def _list_makespan(items, cu_count: int) -> float:
+    """Run time (tile steps) of `items` (costs in the persistent kernel's
+    order): each XCD takes its contiguous share, each of its CUs the next
+    item when free."""
+    total = len(items)
+    q, r = divmod(total, 8)
+    per_xcd = max(1, cu_count // 8)
+    worst = 0.0
+    for x in range(8):
+        lo = x * q + min(x, r)
+        heap = [0.0] * per_xcd
+        for w in range(lo, lo + q + (1 if x < r else 0)):
+            heapq.heapreplace(heap, heap[0] + items[w])
+        worst = max(worst, max(heap))
+    return worst
+
+
+def chunks_makespan(tiles, kv_splits: int, n_bh: int, cu_count: int, rows: int, head_dim: int,
+                    causal: bool = True) -> float:
+    """Modelled run time (tile steps) of the single pass over key chunks:
+    items (b, kv head) x chunk x query block (heavy first under causal),
+    chunk c covering tiles [c * ct, (c + 1) * ct) of its block's range, plus
+    the combine (launch and its read of rows x kv_splits partials)."""
+    n = len(tiles)
+    ct = max(1, -(-max(tiles) // kv_splits))
+    order = list(range(n - 1, -1, -1)) if causal else list(range(n))
+    per_bh = [min(ct, max(tiles[m] - c * ct, 0)) + CHUNK_ITEM_OVERHEAD for c in range(kv_splits) for m in order]
+    first = _list_makespan(per_bh * n_bh, cu_count)
+    combine_us = COMBINE_LAUNCH_US + rows * kv_splits * (head_dim + 2) * 4 / COMBINE_BYTES_PER_US
+    return first + combine_us / TILE_STEP_US
+
+
+def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
+                     cu_count: int, causal: bool, head_dim: int = 128, base: float = None) -> int:
+    """Key chunks per query block for the single pass (0: none).
+
+    With fewer query blocks than compute units (chunked prefill or a long
+    verify step against a long cache) most CUs would idle; splitting every
+    block's key range into kv_splits chunks (a power of two, each at least
+    CHUNK_MIN_TILES tiles) fills them, at the cost of the fp32 partials and
+    the combine launch.  Taken when the model beats the single pass (`base`:
+    its modelled time) by FWD_SPLIT_GAIN."""
+    group = num_heads // num_kv_heads
+    block_m = max(1, FWD_ROWS // group)
+    n_mblk = _cdiv(seq_q, block_m)
+    n_bh = batch * num_kv_heads
+    if n_mblk * n_bh >= cu_count or seq_q == 0:
+        return 0
+    tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, seq_kv, causal)
+    if base is None:
+        base = fwd_split_makespan(tiles, 0, n_bh, cu_count, causal)
+    rows = batch * num_heads * seq_q
+    best, best_s = base, 0
+    s = 2
+    while s <= _lib.GQA_MAX_SPLITS and -(-max(tiles) // s) >= CHUNK_MIN_TILES:
+        t = chunks_makespan(tiles, s, n_bh, cu_count, rows, head_dim, causal)
+        if t < best:
+            best, best_s = t, s
+        s *= 2
+    return best_s if best <= (1.0 - FWD_SPLIT_GAIN) * base else 0
+
+
 def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
                      cu_count: int, causal: bool) -> int:
     """Query blocks per (b, kv head) to run as two key halves (0: none).
@@ -145,7 +217,11 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     split-KV kernels; the split count is the power of two that brings the
     first pass to SPLIT_WG_PER_CU workgroups per compute unit, while every
     chunk keeps at least SPLIT_MIN_TILES tiles of SPLIT_TILE keys.  Anything
-    else (prefill, chunked prefill) runs the single-pass kernel.
+    else (prefill, chunked prefill) runs the single-pass kernel: with a key
+    split of its heaviest causal blocks (choose_fwd_split), or, when there
+    are fewer query blocks than compute units, as key chunks combined by the
+    split-KV combine (choose_kv_chunks, route kind "chunks") when the model
+    says that is faster.
     """
     group = num_heads // num_kv_heads
     rows = group * seq_q
@@ -159,6 +235,16 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
             splits *= 2
         return Route("split", splits, base * splits)
     ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal)
+    # Key chunks, against the better of the plain and the block-split single pass.
+    # (Only from SPLIT_MIN_KV keys on, the length from which the reference
+    # splits the key axis at all.)
+    n_mblk = _cdiv(seq_q, max(1, FWD_ROWS // group))
+    if n_mblk * num_kv_heads * batch < cu_count and seq_q > 0 and seq_kv >= SPLIT_MIN_KV:
+        tiles = _fwd_block_tiles(n_mblk, max(1, FWD_ROWS // group), seq_q, seq_kv, causal)
+        base = fwd_split_makespan(tiles, ns, num_kv_heads * batch, cu_count, causal)
+        kc = choose_kv_chunks(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal, head_dim, base)
+        if kc:
+            return Route("chunks", kc, single_wgs * kc)
     return Route("single", 1, single_wgs + ns * num_kv_heads * batch, ns)
 
 
@@ -242,6 +328,8 @@ def _launch(route, q_in, k, v, causal, return_lse, dev):
     o = torch.empty_like(q_in)  # as dispatch.py:47; contiguous if unusable
     if not _is_kernel_ready(o):
         o = torch.empty_like(q_in, memory_format=torch.contiguous_format)
+    if route.kind == "chunks":
+        return chunks_forward(q, k, v, o, causal, route.splits, return_lse)
     return single_pass_forward(q, k, v, o, causal, route.fwd_split, return_lse)
 
 
@@ -270,4 +358,26 @@ def single_pass_forward(q, k, v, o, causal, fwd_split=0, return_lse=False):
                                lib.gqa_fwd_split_workspace_bytes(batch, num_kv_heads, head_dim, fwd_split))
     _lib.check(lib.gqa_fwd_split_launch(*qkvo, None if lse is None else lse.data_ptr(),
                                         None if ws is None else ws.data_ptr(), cnt.data_ptr(), fwd_split, *common))
+    return o if lse is None else (o, lse)
+
+
+def chunks_forward(q, k, v, o, causal, kv_splits, return_lse=False):
+    """Launch the single pass over key chunks on kernel-ready q, k, v and
+    output o through gqa_fwd_chunks_launch: every query block runs as
+    kv_splits work items over consecutive key ranges, each writing fp32
+    partials into the stream's cached split workspace, which the split-KV
+    combine reduces into o (and lse)."""
+    lib = _lib.load()
+    batch, num_heads, seq_q, head_dim = q.shape
+    _, num_kv_heads, seq_kv, _ = k.shape
+    stream = stream_handle(q.device)
+    ws = _workspace_buffer(q.device, stream,
+                           lib.gqa_split_workspace_bytes(batch, num_heads, seq_q, head_dim, kv_splits))
+    cnt = _counter_buffer(q.device, stream, lib.gqa_fwd_split_counters_count(batch, num_kv_heads, 0))
+    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
+    _lib.check(lib.gqa_fwd_chunks_launch(
+        q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k), v.data_ptr(), _lib.strides(v),
+        o.data_ptr(), _lib.strides(o), None if lse is None else lse.data_ptr(), ws.data_ptr(), cnt.data_ptr(),
+        kv_splits, batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, (head_dim ** -0.5) * LOG2E,
+        int(bool(causal)), _DTYPES[q.dtype], stream))
     return o if lse is None else (o, lse)

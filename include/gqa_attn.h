@@ -137,6 +137,32 @@ int gqa_fwd_split_launch(const void* q, const int64_t q_stride[4],
                          int seq_q, int seq_kv, int head_dim,
                          float scale_log2, int causal, int dtype, void* stream);
 
+/* Single pass over key chunks, then the split-KV combine (no counterpart in
+ * the reference, whose dispatch.py:47-61 runs these shapes as one program
+ * per query block over all keys).  For query blocks longer than the split
+ * path takes (more than 64 packed rows per kv head: chunked prefill, long
+ * verify steps) against a long key cache, one work item per query block
+ * leaves most compute units idle (a 128-token chunk of Llama-3.1-8B:
+ * 16 items).  Here every query block of 256 packed rows runs as kv_splits
+ * work items over consecutive ranges of ceil(ceil(seq_kv / 64) / kv_splits)
+ * 64-key tiles, each writing the fp32 partial (m in log2 units, l,
+ * unnormalised acc) of its rows into the split-KV workspace layout; the
+ * split-KV combine (gqa_split_reduce_launch's kernel) then writes o and,
+ * when lse is not NULL, the LSE as gqa_fwd_lse_launch.  Results equal
+ * gqa_fwd_launch's up to float rounding.  kv_splits in [1, GQA_MAX_SPLITS];
+ * workspace: gqa_split_workspace_bytes(batch, num_heads, seq_q, head_dim,
+ * kv_splits) bytes, 16-byte aligned; counters: NULL (static schedule) or
+ * gqa_fwd_split_counters_count(batch, num_kv_heads, 0) int32, zero on the
+ * first call and left zero (as gqa_fwd_split_launch's). */
+int gqa_fwd_chunks_launch(const void* q, const int64_t q_stride[4],
+                          const void* k, const int64_t k_stride[4],
+                          const void* v, const int64_t v_stride[4],
+                          void* o, const int64_t o_stride[4], float* lse,
+                          float* workspace, int* counters, int kv_splits,
+                          int batch, int num_heads, int num_kv_heads,
+                          int seq_q, int seq_kv, int head_dim,
+                          float scale_log2, int causal, int dtype, void* stream);
+
 /* Bytes of fp32 workspace the split-KV path needs for `splits` chunks:
  * acc (batch, num_heads, seq_q, splits, head_dim) followed by m and l
  * (batch, num_heads, seq_q, splits) each — the partial tensors of reference

@@ -150,6 +150,24 @@ def test_split_launch_validation(lib):
     assert r(_FAKE, 8, _FAKE, _BAD, 1, 32, 1, 128, 0, None) == -4
 
 
+def test_chunks_launch_validation(lib):
+    f = lib.gqa_fwd_chunks_launch
+    args = lambda ws, cnt, splits, lse=None, B=1, Sq=128: (
+        _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, lse, ws, cnt, splits,
+        B, 32, 8, Sq, 4096, 128, 0.1, 1, 0, None)
+    assert f(*args(_FAKE, None, 0)) == -5
+    assert f(*args(_FAKE, None, 2048)) == -5
+    assert f(*args(None, None, 8)) == -7
+    assert f(*args(ctypes.c_void_p((1 << 20) + 4), None, 8)) == -4    # workspace alignment
+    assert f(*args(_FAKE, ctypes.c_void_p((1 << 20) + 2), 8)) == -4   # counters alignment
+    assert f(*args(_FAKE, None, 8, lse=ctypes.c_void_p((1 << 20) + 2))) == -4
+    assert f(*args(None, None, 8, B=0)) == 0   # nothing to do
+    assert f(*args(None, None, 8, Sq=0)) == 0
+    bad = (_FAKE, _BAD, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, None, _FAKE, None, 8,
+           1, 32, 8, 128, 4096, 128, 0.1, 1, 0, None)
+    assert f(*bad) == -4
+
+
 # ---------------------------------------------------------------------------
 # Dispatch rule
 # ---------------------------------------------------------------------------
@@ -192,10 +210,36 @@ def test_route_wide_row_blocks():
         r64 = choose_route(1, 32, 8, sq, 131072, cu, True, 64)
         assert r64.kind == "split" and r64.splits == 32 and r64.workgroups == 512
     assert choose_route(1, 32, 8, 8, 131072, cu).workgroups == 512
-    assert choose_route(1, 32, 8, 17, 131072, cu).kind == "single"
+    assert choose_route(1, 32, 8, 17, 131072, cu).kind == "chunks"  # past the split path: key chunks
     assert paged_splits(1, 32, 8, 16, 131072, cu) == 64
     assert paged_splits(1, 32, 8, 16, 131072, cu, block_size=16) == 64
     assert paged_splits(1, 32, 8, 16, 131072, cu, head_dim=64) == 32
+
+
+def test_route_key_chunks():
+    # Fewer query blocks than compute units against a long cache: the
+    # single pass over key chunks (one item per block and chunk) when the
+    # model beats the plain single pass; never for the BASELINE prefill
+    # shapes, below the reference's 1024-key split threshold, or with a
+    # compute unit per block already.
+    from gqa_kernels.dispatch import (CHUNK_MIN_TILES, _fwd_block_tiles, choose_kv_chunks, choose_route,
+                                      chunks_makespan, fwd_split_makespan)
+    cu = 256
+    r = choose_route(1, 32, 8, 128, 131072, cu)
+    assert r.kind == "chunks" and r.splits == 16 and r.workgroups == 256
+    r = choose_route(1, 32, 8, 512, 32768, cu)
+    assert r.kind == "chunks" and r.splits == 4
+    for S in (2048, 4096, 8192, 16384):
+        assert choose_route(1, 32, 8, S, S, cu).kind == "single"
+    assert choose_route(4, 32, 8, 512, 8192, cu).kind == "single"   # 256 blocks
+    assert choose_route(1, 32, 8, 200, 900, cu).kind == "single"    # below 1024 keys
+    assert choose_route(1, 32, 8, 2048, 131072, cu).kind == "single"
+    # the model: chunk counts are powers of two with >= CHUNK_MIN_TILES tiles
+    tiles = _fwd_block_tiles(2, 64, 128, 131072, True)
+    base = fwd_split_makespan(tiles, 0, 8, cu)
+    kc = choose_kv_chunks(1, 32, 8, 128, 131072, cu, True)
+    assert kc & (kc - 1) == 0 and -(-max(tiles) // kc) >= CHUNK_MIN_TILES
+    assert chunks_makespan(tiles, kc, 8, cu, 32 * 128, 128) < 0.1 * base
 
 
 def test_fwd_split_choice():
