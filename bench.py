@@ -9,7 +9,8 @@ KV cache (gqa_kernels.paged) at two block sizes / in-block layouts,
 ``paged_prefill`` the chunked-prefill shape over a paged cache, and
 ``configs`` every BASELINE config (prefill 2048-16384, decode 2048-131072,
 chunked prefill, the 70B decode shape) with its time and the fraction of the
-roofline (MFMA or HBM) that bounds it; HBM-bound configs rotate K/V sets so
+roofline (MFMA or HBM) that bounds it, ``extras`` the same for a 16-token
+verify step and a 128-token chunk against 131072 keys; HBM-bound configs rotate K/V sets so
 the Infinity Cache cannot serve a call from the previous one.  Timing
 follows reference benchmark/run.py:140-154 (untimed warm-up calls, then
 back-to-back calls of the full public function between two events on the
@@ -249,12 +250,14 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
     ap.add_argument("--config", default=None,
                     help="with --only configs: time only the BASELINE configs whose name starts with this")
-    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b", "configs"],
+    ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b", "configs",
+                                       "extras"],
                     default=None,
                     help="time one workload only (for profiling runs); 'copy' times a plain 1 GiB "
                          "device copy, the calibration kernel of the HBM traffic counters; 'gemm' "
                          "a 16384^3 bf16 library GEMM, the practical MFMA ceiling of the box; "
-                         "'chunked' and '70b' one BASELINE config each; 'configs' every BASELINE config")
+                         "'chunked' and '70b' one BASELINE config each; 'configs' every BASELINE config; "
+                         "'extras' the verify-step and key-chunk shapes")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -357,6 +360,9 @@ def main() -> int:
     # ---------------- every BASELINE config ----------------
     if args.only is None:
         result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup)
+        result["extras"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup, table=EXTRAS)
+    elif args.only == "extras":
+        result["extras"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup, table=EXTRAS)
     elif args.only in ("chunked", "70b"):
         result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup,
                                   only={"chunked": "chunked", "70b": "70B"}[args.only])
@@ -443,12 +449,20 @@ CONFIGS = (
        ("70B decode B=16 Hq=64 Sq=4 32768", 16, 64, 8, 4, 32768, "hbm", 128),
        ("prefill 16384 head_dim 64", 1, 32, 8, 16384, 16384, "mfma", 64)]
 )
+# Shapes beyond the BASELINE configs that exercise the other routes (timed
+# in the default run as ``extras``): a verify step of 16 tokens (64 packed
+# rows per kv head: the decode first pass with 64-row workgroups) and a
+# 128-token chunk (the single pass over key chunks), both against 131072 keys.
+EXTRAS = (
+    ("verify 16 x 131072", 1, 32, 8, 16, 131072, "hbm", 128),
+    ("chunk 128 x 131072", 1, 32, 8, 128, 131072, "mfma", 128),
+)
 # K/V sets rotated per HBM-bound config: enough that consecutive calls cannot
 # find the previous calls' keys in the 256 MB Infinity Cache.
 ROTATE_BYTES = 600e6
 
 
-def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None):
+def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None, table=CONFIGS):
     """Time every BASELINE config (or the one named `only`, else the ones
     whose name starts with it): mean µs over `steps` back-to-back calls (5x as many for
     HBM-bound configs, which take microseconds) after `warmup` calls, with
@@ -456,9 +470,9 @@ def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None):
     config.  HBM-bound configs rotate K/V sets (ROTATE_BYTES in total)."""
     from gqa_kernels.dispatch import _cu_count, choose_route
     rows = []
-    sel = CONFIGS
+    sel = table
     if only is not None:  # the config of that exact name, else those starting with it
-        sel = [c for c in CONFIGS if c[0] == only] or [c for c in CONFIGS if c[0].startswith(only)]
+        sel = [c for c in table if c[0] == only] or [c for c in table if c[0].startswith(only)]
     for name, b, hq, hkv, sq, skv, bound, d in sel:
         by1 = hbm_bytes(b, hq, hkv, sq, skv, d)
         nset = max(1, math.ceil(ROTATE_BYTES / by1)) if bound == "hbm" else 1
@@ -472,7 +486,7 @@ def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None):
         route = choose_route(b, hq, hkv, sq, skv, _cu_count(0))
         rows.append({"config": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv, "D": d,
                      "us": ms * 1e3, "tflops": tflops, "gbs": gbs, "steps": n, "kv_sets": nset,
-                     "route": route.kind + (f" splits={route.splits}" if route.kind == "split" else
+                     "route": route.kind + (f" splits={route.splits}" if route.kind in ("split", "chunks") else
                                             f" key-split blocks={route.fwd_split}" if route.fwd_split else ""),
                      "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                                   "frac": achieved / peak, "flops_per_call": fl, "bytes_per_call": by1}})
