@@ -25,11 +25,13 @@
 // no cross-wave merge.  With a decode group of 4 query rows most of each
 // S^T MFMA is padding; it runs hidden under the HBM stream.
 //
-// Wide row blocks (RW = 2, for 33-64 packed rows per kv head, e.g. verify
-// steps of 9-16 tokens at G = 4): one workgroup takes two 32-row blocks, so
-// the chunk's K/V stream once instead of once per 32-row block.  Waves 2h
-// and 2h + 1 take rows [32h, 32h + 32) of the block, each with 64 of the
-// 128 dims; partials and the fused combine stay per 32-row block.
+// Wide row blocks (RW = 2 or 4, for 33-64 or 65-128 packed rows per kv
+// head, e.g. verify steps of 9-16 or 17-32 tokens at G = 4): one workgroup
+// takes RW 32-row blocks, so the chunk's K/V stream once instead of once
+// per 32-row block.  RW = 2: waves 2h and 2h + 1 take rows [32h, 32h + 32)
+// of the block, each with 64 of the 128 dims; RW = 4: wave h takes rows
+// [32h, 32h + 32) with all 128 dims.  Partials and the fused combine stay
+// per 32-row block.
 //
 // Fused combine (SplitParams::counters set): the last workgroup of each
 // (b, kv head, row block) to count its partial in combines all splits
@@ -212,7 +214,7 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
 // (SplitParams::k/v: sb = block, ss = slot, sh = head stride); sequence b has
 // min(seq_lens[b], Skv) keys.  With q_start / q_len set, q is token-major and
 // sequence b has q_len[b] query rows from token q_start[b].
-// RW: 32-row blocks per workgroup (1 or 2).
+// RW: 32-row blocks per workgroup (1, 2 or 4).
 template <int DT, int KV, int RW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_decode_kernel(SplitParams p) {
   constexpr int D = kDecD;
@@ -238,12 +240,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;
   const int i = lane & 31, hh = lane >> 5;
-  // This wave's 32-row half of the block (rh) and its NDB 32-dim blocks of
-  // O^T from db0: RW = 1, dim block `wave`; RW = 2, dim blocks 2 (wave & 1)
-  // and 2 (wave & 1) + 1.
+  // This wave's 32-row block within the workgroup's (rh) and its NDB 32-dim
+  // blocks of O^T from db0: RW = 1, dim block `wave`; RW = 2, dim blocks
+  // 2 (wave & 1) and 2 (wave & 1) + 1; RW = 4, all four.
   constexpr int NDB = RW;
-  const int rh = RW == 2 ? wave >> 1 : 0;
-  const int db0 = RW == 2 ? 2 * (wave & 1) : wave;
+  constexpr int WPR = 4 / RW;  // waves per 32-row block
+  const int rh = wave / WPR;
+  const int db0 = (wave % WPR) * RW;
 
   const int n_wblk = (p.n_rblk + RW - 1) / RW;
   const int total = dm.B * dm.Hkv * n_wblk * p.splits;
@@ -603,14 +606,16 @@ bool decode_kernel_fits(const SplitParams& p) {
   return acc_bytes <= 0xFFFFFFF0ll && q_bytes < ((int64_t)1 << 31);
 }
 
-// Two 32-row blocks per workgroup whenever a kv head has more than one
-// (each K/V chunk is then streamed once per 64 rows, not per 32).
+// Every 32-row block of a kv head in one workgroup up to four (each K/V
+// chunk is then streamed once per 64 or 128 rows, not per 32).
 template <int DT, int KV>
 static hipError_t launch_decode_t(const SplitParams& p, hipStream_t stream) {
-  const int rw = p.n_rblk >= 2 ? 2 : 1;
+  const int rw = p.n_rblk >= 3 ? 4 : p.n_rblk == 2 ? 2 : 1;
   const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * ((p.n_rblk + rw - 1) / rw) * p.splits;
   if (total <= 0) return hipSuccess;
-  if (rw == 2)
+  if (rw == 4)
+    hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 4>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  else if (rw == 2)
     hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 2>), dim3((unsigned)total), dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 1>), dim3((unsigned)total), dim3(256), 0, stream, p);

@@ -28,8 +28,17 @@ SPLIT_ROWS = 32
 # At head_dim 128 one split-KV workgroup takes two row blocks when a kv head
 # has more than one (each K/V chunk is then streamed once per 64 rows).
 SPLIT_WIDE_ROWS = 64
-# The split-KV path is taken for at most this many packed rows per kv head.
+# ... and all of them up to four (65-128 rows).
+SPLIT_WIDER_ROWS = 128
+# The split-KV path is taken for at most this many packed rows per kv head
+# (at head_dim 128: SPLIT_WIDER_ROWS).
 SPLIT_MAX_ROWS = 64
+# With 128-row workgroups the split count first fills the compute units
+# (chunks of at least SPLIT_TILE keys), then doubles toward SPLIT_WG_PER_CU
+# workgroups per CU only while chunks keep at least this many keys (each
+# tile costs a 128-row workgroup 32 MFMAs per wave; shorter chunks measured
+# slower: 32 tokens x 32768 keys, 256 workgroups 41 us, 512 51 us).
+SPLIT_WIDER_MIN_CHUNK = 1024
 # Shortest key cache worth splitting (the reference's threshold, dispatch.py:37).
 SPLIT_MIN_KV = 1024
 # Keys per split-KV tile; a chunk is never shorter than this many tiles
@@ -203,8 +212,33 @@ def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
 
 def split_rows_per_workgroup(rows: int, head_dim: int = 128) -> int:
     """Packed rows one split-KV workgroup covers (the first pass's row
-    blocks: 32, or two of them at head_dim 128)."""
-    return SPLIT_WIDE_ROWS if head_dim == 128 and rows > SPLIT_ROWS else SPLIT_ROWS
+    blocks: 32, or at head_dim 128 two or four of them)."""
+    if head_dim != 128 or rows <= SPLIT_ROWS:
+        return SPLIT_ROWS
+    return SPLIT_WIDE_ROWS if rows <= SPLIT_WIDE_ROWS else SPLIT_WIDER_ROWS
+
+
+def split_max_rows(head_dim: int = 128) -> int:
+    """Packed rows per kv head up to which the split-KV path is taken."""
+    return SPLIT_WIDER_ROWS if head_dim == 128 else SPLIT_MAX_ROWS
+
+
+def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int) -> int:
+    """Split count of the split-KV path for `base` workgroups per split."""
+    target = SPLIT_WG_PER_CU * cu_count
+    splits = 1
+    if rows_per_wg > SPLIT_WIDE_ROWS:
+        while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
+               and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
+            splits *= 2
+        while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
+               and _cdiv(seq_kv, splits * 2) >= SPLIT_WIDER_MIN_CHUNK):
+            splits *= 2
+        return splits
+    while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
+           and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
+        splits *= 2
+    return splits
 
 
 def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
@@ -212,11 +246,12 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     """Pick the kernel path for one call (pure function of the shapes).
 
     Counterpart of reference dispatch.py:35-45.  A query block of at most
-    SPLIT_MAX_ROWS packed rows per kv head (e.g. decode: group * seq_q = 4)
+    split_max_rows(head_dim) packed rows per kv head (decode: group * seq_q = 4)
     against a cache of at least SPLIT_MIN_KV keys streams K/V with the
     split-KV kernels; the split count is the power of two that brings the
     first pass to SPLIT_WG_PER_CU workgroups per compute unit, while every
-    chunk keeps at least SPLIT_MIN_TILES tiles of SPLIT_TILE keys.  Anything
+    chunk keeps at least SPLIT_MIN_TILES tiles of SPLIT_TILE keys (with
+    128-row workgroups: split_count).  Anything
     else (prefill, chunked prefill) runs the single-pass kernel: with a key
     split of its heaviest causal blocks (choose_fwd_split), or, when there
     are fewer query blocks than compute units, as key chunks combined by the
@@ -226,13 +261,10 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     group = num_heads // num_kv_heads
     rows = group * seq_q
     single_wgs = _cdiv(seq_q, max(1, FWD_ROWS // group)) * num_kv_heads * batch
-    if rows <= SPLIT_MAX_ROWS and seq_kv >= SPLIT_MIN_KV:
-        base = _cdiv(rows, split_rows_per_workgroup(rows, head_dim)) * num_kv_heads * batch
-        target = SPLIT_WG_PER_CU * cu_count
-        splits = 1
-        while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
-               and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
-            splits *= 2
+    if rows <= split_max_rows(head_dim) and seq_kv >= SPLIT_MIN_KV:
+        rpw = split_rows_per_workgroup(rows, head_dim)
+        base = _cdiv(rows, rpw) * num_kv_heads * batch
+        splits = split_count(base, seq_kv, cu_count, rpw)
         return Route("split", splits, base * splits)
     ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal)
     # Key chunks, against the better of the plain and the block-split single pass.

@@ -60,6 +60,8 @@ _SPLIT_ROWS = 32
 _SPLIT_WG_PER_CU = 2
 _MIN_CHUNK = 256
 _SPLIT_MAX_ROWS = 64  # packed rows per kv head up to which the split-KV pass is used
+_SPLIT_MAX_ROWS_WIDE = 128  # ... at head_dim 128 with pages of >= 4 keys (128-row workgroups)
+_WIDE_MIN_CHUNK = 1024
 
 _cu_lock = threading.Lock()
 _cu_counts: dict = {}
@@ -92,15 +94,27 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
     workgroup stages in LDS), which can ask for more splits."""
     group = num_heads // num_kv_heads
     rows = group * seq_q
-    # Rows per first-pass workgroup: two 32-row blocks at head_dim 128 with
-    # pages of >= 4 keys (the LDS-DMA first pass), else one.
-    wide = head_dim == 128 and block_size >= 4 and rows > _SPLIT_ROWS
-    base = -(-rows // (2 * _SPLIT_ROWS if wide else _SPLIT_ROWS)) * num_kv_heads * batch
+    # Rows per first-pass workgroup: up to four 32-row blocks at head_dim 128
+    # with pages of >= 4 keys (the LDS-DMA first pass), else one.
+    rpw = _SPLIT_ROWS
+    if head_dim == 128 and block_size >= 4 and rows > _SPLIT_ROWS:
+        rpw = 2 * _SPLIT_ROWS if rows <= 2 * _SPLIT_ROWS else 4 * _SPLIT_ROWS
+    base = -(-rows // rpw) * num_kv_heads * batch
     target = _SPLIT_WG_PER_CU * cu_count
     splits = 1
-    while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
-           and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
-        splits *= 2
+    if rpw > 2 * _SPLIT_ROWS:
+        # 128-row workgroups: fill the compute units, then more splits only
+        # while chunks keep _WIDE_MIN_CHUNK keys (as the contiguous route).
+        while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
+               and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
+            splits *= 2
+        while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
+               and -(-max_seq_len // (splits * 2)) >= _WIDE_MIN_CHUNK):
+            splits *= 2
+    else:
+        while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
+               and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
+            splits *= 2
     if block_size < 64:
         def too_many_pages(s):
             return paged_chunk(max_seq_len, s) // block_size > _lib.GQA_PAGED_CHUNK_PAGES
@@ -143,7 +157,8 @@ def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int, 
     contiguous decode route; "single" (the single-pass kernel loading each
     tile from its blocks) for longer ones when blocks hold at least
     single_pass_min_block(head_dim) keys."""
-    if (num_heads // num_kv_heads) * seq_q <= _SPLIT_MAX_ROWS or block_size < single_pass_min_block(head_dim):
+    max_rows = _SPLIT_MAX_ROWS_WIDE if head_dim == 128 and block_size >= 4 else _SPLIT_MAX_ROWS
+    if (num_heads // num_kv_heads) * seq_q <= max_rows or block_size < single_pass_min_block(head_dim):
         return "split"
     return "single"
 

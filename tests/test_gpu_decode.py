@@ -58,12 +58,17 @@ def test_decode_g8_rows_fill_a_block():
     (64, 8, 5, 1000, 2),              # G = 8: 40 rows
     (32, 8, 12, 256, 8),              # 32-key chunks: the causal diagonal crosses chunks
     (32, 8, 16, 10, 2),               # seq_q > seq_kv: rows of positions 0-5 see no key (NaN)
+    (32, 8, 17, 3 * 64 * 5 + 11, 4),  # 68 rows: four blocks per workgroup, the last holding 4 rows
+    (32, 8, 32, 4096, 8),             # 128 rows: four full blocks
+    (12, 4, 30, 2000, 3),             # G = 3, 90 rows: three blocks, the fourth empty
+    (64, 8, 16, 1000, 2),             # G = 8: 128 rows
+    (32, 8, 32, 20, 2),               # seq_q > seq_kv with four blocks: positions 0-11 see no key
 ])
 @pytest.mark.parametrize("fused", [False, True])
 def test_decode_wide_row_blocks(Hq, Hkv, sq, skv, S, fused):
-    # 33-64 packed rows per kv head: one workgroup covers two 32-row blocks
-    # (waves 0-1 the first, 2-3 the second), streaming each chunk once; the
-    # partials and the combine stay per 32-row block.
+    # 33-128 packed rows per kv head: one workgroup covers two or four
+    # 32-row blocks (waves 0-1 / 2-3, or one wave each), streaming each
+    # chunk once; the partials and the combine stay per 32-row block.
     from gqa_kernels.gqa_split import split_kv_forward
     from oracle.gqa_oracle import gqa_lse
     q, k, v = make_inputs(1, Hq, Hkv, sq, skv, 128, torch.bfloat16, seed=sq * skv + S, device=DEV)

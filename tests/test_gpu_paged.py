@@ -81,6 +81,7 @@ def _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype):
     (3, 32, 8, 1, [0, 500, 64], 128, 16, torch.bfloat16, True),           # a sequence without keys: zeros
     (2, 32, 8, 16, [3000, 700], 128, 16, torch.bfloat16, True),           # 64 rows: one wide row block
     (3, 32, 8, 9, [1300, 64, 5], 128, 64, torch.float16, True),           # 36 rows, a sequence shorter than Sq
+    (2, 32, 8, 32, [2500, 40], 128, 16, torch.bfloat16, True),            # 128 rows: four blocks per workgroup
 ])
 def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal):
     from gqa_kernels.paged import paged_attention

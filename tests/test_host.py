@@ -210,7 +210,16 @@ def test_route_wide_row_blocks():
         r64 = choose_route(1, 32, 8, sq, 131072, cu, True, 64)
         assert r64.kind == "split" and r64.splits == 32 and r64.workgroups == 512
     assert choose_route(1, 32, 8, 8, 131072, cu).workgroups == 512
-    assert choose_route(1, 32, 8, 17, 131072, cu).kind == "chunks"  # past the split path: key chunks
+    # 65-128 rows: four 32-row blocks per workgroup; the split count fills
+    # the CUs, then doubles only while chunks keep 1024 keys
+    r = choose_route(1, 32, 8, 17, 131072, cu)
+    assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
+    assert choose_route(1, 32, 8, 32, 32768, cu).splits == 32
+    assert choose_route(4, 32, 8, 32, 32768, cu).splits == 16
+    assert split_rows_per_workgroup(65) == 128 and split_rows_per_workgroup(128) == 128
+    assert choose_route(1, 32, 8, 33, 131072, cu).kind == "chunks"  # past the split path: key chunks
+    assert choose_route(1, 32, 8, 17, 131072, cu, True, 64).kind == "chunks"  # head_dim 64: 64 rows at most
+    assert paged_splits(1, 32, 8, 32, 32768, cu) == 32
     assert paged_splits(1, 32, 8, 16, 131072, cu) == 64
     assert paged_splits(1, 32, 8, 16, 131072, cu, block_size=16) == 64
     assert paged_splits(1, 32, 8, 16, 131072, cu, head_dim=64) == 32

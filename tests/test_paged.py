@@ -198,13 +198,15 @@ def test_paged_route():
     from gqa_kernels.paged import paged_route
     assert paged_route(32, 8, 1, 16) == "split"      # decode
     assert paged_route(32, 8, 16, 64) == "split"     # 64 packed rows
-    assert paged_route(32, 8, 17, 64) == "single"
+    assert paged_route(32, 8, 32, 64) == "split"     # 128 packed rows: four blocks per workgroup at D = 128
+    assert paged_route(32, 8, 33, 64) == "single"
+    assert paged_route(32, 8, 17, 64, 64) == "single"  # D = 64: 64 packed rows at most
     assert paged_route(32, 8, 512, 16) == "single"   # 16-key blocks: one descriptor per 4-row instruction
     assert paged_route(32, 8, 512, 4) == "single"
     assert paged_route(32, 8, 512, 2) == "split"     # below one instruction's rows at D = 128
     assert paged_route(32, 8, 512, 4, 64) == "split"  # D = 64: 8 rows per instruction
     assert paged_route(32, 8, 512, 8, 64) == "single"
-    assert paged_route(64, 8, 9, 128) == "single"
+    assert paged_route(64, 8, 17, 128) == "single"
 
 
 def test_strerror_block(lib):
