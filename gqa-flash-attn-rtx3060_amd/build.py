@@ -3,7 +3,9 @@
 Usage: python gqa-flash-attn-rtx3060_amd/build.py [-v]
 
 Each csrc/*.hip file is compiled to an object in parallel, then linked into
-gqa_kernels/libgqa_hip.so next to the Python package that loads it.  The
+gqa_kernels/libgqa_hip.so next to the Python package that loads it; then
+csrc/host/gqa_host.cpp (the torch-tensor binding of the decode call) is
+built into gqa_kernels/_gqa_host.so against it.  The
 build always runs (no up-to-date check): callers that need the library to
 match the sources call this after every source change.
 """
@@ -21,6 +23,7 @@ REPO_ROOT = PKG_ROOT.parent
 CSRC = PKG_ROOT / "csrc"
 OBJ_DIR = PKG_ROOT / "_build"
 LIB_PATH = PKG_ROOT / "gqa_kernels" / "libgqa_hip.so"
+HOST_PATH = PKG_ROOT / "gqa_kernels" / "_gqa_host.so"
 
 ARCH = "gfx950"
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
@@ -77,7 +80,35 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
+    build_host(verbose)
     return LIB_PATH
+
+
+def build_host(verbose: bool = False) -> Path:
+    """The torch-tensor binding of the decode call (csrc/host/gqa_host.cpp):
+    host-only C++ built with g++ against torch's headers, linked to
+    libgqa_hip.so beside it (rpath $ORIGIN), as gqa_kernels/_gqa_host.so."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    src = CSRC / "host" / "gqa_host.cpp"
+    tmp = HOST_PATH.with_suffix(".so.tmp")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-shared", str(src), "-o", str(tmp),
+           f"-I{REPO_ROOT / 'include'}", f"-I{sysconfig.get_paths()['include']}",
+           *[f"-I{p}" for p in cpp_extension.include_paths()],
+           f"-I{os.environ.get('ROCM_PATH', '/opt/rocm')}/include",
+           # the HIP runtime headers, included through torch's, select the
+           # AMD platform from this macro when not compiled by hipcc
+           "-D__HIP_PLATFORM_AMD__", "-DTORCH_EXTENSION_NAME=_gqa_host", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-L{p}" for p in cpp_extension.library_paths()], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", f"-L{LIB_PATH.parent}", "-lgqa_hip", "-Wl,-rpath,$ORIGIN"]
+    _run(cmd, verbose)
+    os.replace(tmp, HOST_PATH)
+    return HOST_PATH
 
 
 if __name__ == "__main__":

@@ -133,6 +133,34 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+HOST_PATH = Path(__file__).resolve().parent / "_gqa_host.so"
+_host = None
+
+
+def load_host():
+    """Load (once) and return the torch-tensor binding of the decode call
+    (``_gqa_host.so``, built beside the library by build.py); raises if it
+    is missing or was built against another library ABI."""
+    global _host
+    if _host is not None:
+        return _host
+    load()  # the library it links against, checked first (takes _lock itself)
+    with _lock:
+        if _host is not None:
+            return _host
+        import importlib.util
+
+        if not HOST_PATH.exists():
+            raise RuntimeError(f"{HOST_PATH} not found: build it with `python gqa-flash-attn-rtx3060_amd/build.py`")
+        spec = importlib.util.spec_from_file_location("gqa_kernels._gqa_host", str(HOST_PATH))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        if mod.ABI_VERSION != ABI_VERSION:
+            raise RuntimeError(f"_gqa_host.so built against ABI {mod.ABI_VERSION} != {ABI_VERSION}; rebuild")
+        _host = mod
+        return mod
+
+
 def check(code: int) -> None:
     """Raise GQAError with the library's message for a non-zero return code."""
     if code != 0:

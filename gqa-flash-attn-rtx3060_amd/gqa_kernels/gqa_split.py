@@ -102,22 +102,16 @@ def decode_forward(q, k, v, causal, splits, return_lse, dev):
     splits, return_lse=return_lse) does, with the host work of a decode step
     kept to one pass over the arguments (every value read once)."""
     batch, num_heads, seq_q, head_dim = q.shape
-    _, num_kv_heads, seq_kv, _ = k.shape
     stream = _raw_stream(dev) if _raw_stream is not None else torch.cuda.current_stream(dev).cuda_stream
     need = batch * num_heads * seq_q * splits * (head_dim + 2) * 4
     ws = _workspaces.get((dev, stream))
     if ws is None or ws.numel() * 4 < need:
         ws = _workspace_buffer(q.device, stream, need)
-    o = torch.empty_like(q)
-    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
-    rc = _lib.load().gqa_split_launch(
-        q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k), v.data_ptr(), _lib.strides(v),
-        o.data_ptr(), _lib.strides(o), None if lse is None else lse.data_ptr(), ws.data_ptr(), splits,
-        batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, _SCALE_LOG2[head_dim], 1 if causal else 0,
-        _DTYPES[q.dtype], stream)
-    if rc:
-        _lib.check(rc)
-    return o if lse is None else (o, lse)
+    # gqa_split_launch through the torch-tensor binding (_gqa_host.so): the
+    # argument marshalling of a decode step in C++ rather than ctypes.
+    host = _lib._host if _lib._host is not None else _lib.load_host()
+    return host.split_decode(q, k, v, ws, splits, bool(causal), _SCALE_LOG2[head_dim], _DTYPES[q.dtype],
+                             bool(return_lse))
 
 
 def split_kv_forward(q, k, v, causal, splits, workspace=None, fused=False, return_lse=False):

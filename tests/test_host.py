@@ -62,6 +62,17 @@ def test_abi_version_and_strerror(lib):
     assert b"head_dim" in lib.gqa_strerror(-2)
 
 
+def test_host_binding_loads(lib):
+    """The torch-tensor binding of the decode call (_gqa_host.so) loads,
+    links against the same library ABI and exposes split_decode (no GPU
+    work: the binding is exercised by the GPU decode tests)."""
+    from gqa_kernels import _lib
+    host = _lib.load_host()
+    assert host.ABI_VERSION == lib.gqa_abi_version() == _lib.ABI_VERSION
+    assert callable(host.split_decode)
+    assert _lib.load_host() is host
+
+
 def test_workspace_bytes(lib):
     from gqa_kernels.gqa_split import workspace_bytes
     for args in ((1, 32, 1, 128, 128), (16, 64, 4, 128, 8), (2, 8, 3, 64, 7)):
