@@ -33,11 +33,16 @@ SPLIT_WIDER_ROWS = 128
 # The split-KV path is taken for at most this many packed rows per kv head
 # (at head_dim 128: SPLIT_WIDER_ROWS).
 SPLIT_MAX_ROWS = 64
-# With 128-row workgroups the split count first fills the compute units
-# (chunks of at least SPLIT_TILE keys), then doubles toward SPLIT_WG_PER_CU
-# workgroups per CU only while chunks keep at least this many keys (each
-# tile costs a 128-row workgroup 32 MFMAs per wave; shorter chunks measured
-# slower: 32 tokens x 32768 keys, 256 workgroups 41 us, 512 51 us).
+# At head_dim 128 (the decode first pass, gqa_decode_kernel) the split
+# count first fills the compute units with one workgroup each (chunks of at
+# least SPLIT_TILE keys), then doubles toward SPLIT_WG_PER_CU workgroups per
+# CU only while chunks keep at least this many keys: a workgroup's first
+# tiles and Q take 2-3 us to land, which short chunks do not amortise.
+# Measured on MI355X (bf16, rotating K/V sets), one token at G = 4: 16384
+# keys 32 splits 16.9 us / 64 splits 18.0, 32768 keys 27.6 / 29.5, 8192 keys
+# 12.3 / 12.5, 65536 and 131072 keys equal or better at 64; 16 tokens at
+# 32768 keys 35.7 / 41.5; 32 tokens at 32768 keys (128-row workgroups)
+# 256 workgroups 41 us, 512 51 us.
 SPLIT_WIDER_MIN_CHUNK = 1024
 # Shortest key cache worth splitting (the reference's threshold, dispatch.py:37).
 SPLIT_MIN_KV = 1024
@@ -223,11 +228,14 @@ def split_max_rows(head_dim: int = 128) -> int:
     return SPLIT_WIDER_ROWS if head_dim == 128 else SPLIT_MAX_ROWS
 
 
-def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int) -> int:
-    """Split count of the split-KV path for `base` workgroups per split."""
+def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int, head_dim: int = 128) -> int:
+    """Split count of the split-KV path for `base` workgroups per split
+    (head_dim 128: fill the CUs, then a second workgroup per CU only for
+    chunks of SPLIT_WIDER_MIN_CHUNK keys; head_dim 64: two workgroups per CU
+    with chunks of SPLIT_MIN_TILES tiles)."""
     target = SPLIT_WG_PER_CU * cu_count
     splits = 1
-    if rows_per_wg > SPLIT_WIDE_ROWS:
+    if head_dim == 128 or rows_per_wg > SPLIT_WIDE_ROWS:
         while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
                and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
             splits *= 2
@@ -248,10 +256,12 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     Counterpart of reference dispatch.py:35-45.  A query block of at most
     split_max_rows(head_dim) packed rows per kv head (decode: group * seq_q = 4)
     against a cache of at least SPLIT_MIN_KV keys streams K/V with the
-    split-KV kernels; the split count is the power of two that brings the
-    first pass to SPLIT_WG_PER_CU workgroups per compute unit, while every
-    chunk keeps at least SPLIT_MIN_TILES tiles of SPLIT_TILE keys (with
-    128-row workgroups: split_count).  Anything
+    split-KV kernels; the split count is a power of two: at head_dim 128
+    the one that fills the compute units, doubled toward SPLIT_WG_PER_CU
+    workgroups per CU while chunks keep SPLIT_WIDER_MIN_CHUNK keys; at
+    head_dim 64 the one that brings the first pass to SPLIT_WG_PER_CU
+    workgroups per CU, every chunk keeping at least SPLIT_MIN_TILES tiles of
+    SPLIT_TILE keys (split_count).  Anything
     else (prefill, chunked prefill) runs the single-pass kernel: with a key
     split of its heaviest causal blocks (choose_fwd_split), or, when there
     are fewer query blocks than compute units, as key chunks combined by the
@@ -264,7 +274,7 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     if rows <= split_max_rows(head_dim) and seq_kv >= SPLIT_MIN_KV:
         rpw = split_rows_per_workgroup(rows, head_dim)
         base = _cdiv(rows, rpw) * num_kv_heads * batch
-        splits = split_count(base, seq_kv, cu_count, rpw)
+        splits = split_count(base, seq_kv, cu_count, rpw, head_dim)
         return Route("split", splits, base * splits)
     ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal)
     # Key chunks, against the better of the plain and the block-split single pass.
