@@ -50,6 +50,12 @@ PEAK_HBM_GBS = 8000.0
 REF_PREFILL_16K_MS = 96.195
 
 B, HQ, HKV, D = 1, 32, 8, 128
+# The reference benchmark times N(0,1) draws scaled by 0.1 (benchmark/run.py:52-54),
+# the inputs its published numbers were measured on; the timed inputs here
+# follow it.  The shader clock under sustained MFMA load depends on the
+# operands' toggling (x0.1 inputs draw less power than N(0,1)), so the
+# headline is also timed on N(0,1) inputs and reported beside it.
+INPUT_SCALE = 0.1
 PREFILL_S = 16384
 DECODE_S = 131072
 
@@ -71,13 +77,13 @@ def hbm_bytes(b, hq, hkv, sq, skv, d, elem=2) -> int:
     return elem * d * (2 * b * hkv * skv + 2 * b * hq * sq)
 
 
-def _inputs(torch, b, hq, hkv, sq, skv, d, seed=0, n_kv_sets=1):
+def _inputs(torch, b, hq, hkv, sq, skv, d, seed=0, n_kv_sets=1, scale=INPUT_SCALE):
     g = torch.Generator(device="cuda").manual_seed(seed)
-    q = torch.randn(b, hq, sq, d, device="cuda", generator=g).to(torch.bfloat16)
+    q = (torch.randn(b, hq, sq, d, device="cuda", generator=g) * scale).to(torch.bfloat16)
     kvs = []
     for _ in range(n_kv_sets):
-        k = torch.randn(b, hkv, skv, d, device="cuda", generator=g).to(torch.bfloat16)
-        v = torch.randn(b, hkv, skv, d, device="cuda", generator=g).to(torch.bfloat16)
+        k = (torch.randn(b, hkv, skv, d, device="cuda", generator=g) * scale).to(torch.bfloat16)
+        v = (torch.randn(b, hkv, skv, d, device="cuda", generator=g) * scale).to(torch.bfloat16)
         kvs.append((k, v))
     return q, kvs
 
@@ -278,7 +284,8 @@ def main() -> int:
         "metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic N(0,1), seeded torch generator on the GPU",
+        "dtype": "bf16", "data": (f"synthetic N(0,1) x {INPUT_SCALE} (the reference benchmark's inputs, benchmark/run.py:52-54), "
+                 "seeded torch generator on the GPU; unit_normal_inputs: the headline on N(0,1) inputs"),
         "config": {"workload": f"causal GQA prefill B={B} Hq={HQ} Hkv={HKV} D={D} seq={PREFILL_S}",
                    "global_batch": B, "seq_len": PREFILL_S, "parallelism": "single GPU"},
     }
@@ -305,6 +312,14 @@ def main() -> int:
         result["vs_baseline_basis"] = ("speed-up over the reference's published RTX 3060 time for "
                                        f"this workload ({REF_PREFILL_16K_MS} ms)")
         result["gate"] = gate
+        q1, kvs1 = _inputs(torch, B, HQ, HKV, PREFILL_S, PREFILL_S, D, scale=1.0)
+        k1, v1 = kvs1[0]
+        gate1 = _gate(torch, gqa_flash_attn, q1, k1, v1)
+        ms1 = _time(torch, lambda i: gqa_flash_attn(q1, k1, v1, causal=True), args.steps, args.warmup)
+        tf1 = fl / (ms1 * 1e-3) / 1e12
+        result["unit_normal_inputs"] = {"ms_per_step": ms1, "value": tf1, "frac": tf1 / PEAK_BF16_TFLOPS,
+                                        "gate": gate1}
+        del q1, k1, v1, kvs1
         result["roofline"] = {
             "bound": "mfma", "kernel": "gqa_fwd_kernel", "achieved": tflops,
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS,
