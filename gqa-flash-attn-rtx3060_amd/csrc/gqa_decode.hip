@@ -53,6 +53,9 @@ constexpr int kDecTileBytes = FwdStage<kDecD>::kTileBytes;  // one 64-key K or V
 constexpr int kDecBatch = 32;
 // (row, split) pairs of m and l one combining thread loads (R * S <= 4096).
 constexpr int kDecMlPerThread = kFusedMaxRowSplitsHost / 256;
+static_assert(kFusedMaxRowSplitsHost * 4 <= kDecTileBytes, "m (or l) of the fused combine fits one LDS stage");
+static_assert(256 * 16 <= kDecTileBytes && 32 * (kDecD / 4) * 16 <= kDecTileBytes,
+              "the fused combine's split-group sums fit one LDS stage");
 
 // 16-byte device-coherent store (sc1: written through to the point where
 // all XCDs are coherent), through a buffer descriptor over the workspace.
@@ -72,9 +75,11 @@ __device__ inline void store_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t off, f
 //      split groups are added in order in LDS, o = sum / l*.
 // Rows whose chunks are all empty give NaN (m* = -inf), as the reference's
 // combine; a sequence without keys (every split stores m = 0, l = 0) gives
-// zeros.  smem: >= (2 * R * S + 64) floats + nsg * R * D / 4 f32x4.
+// zeros.  LDS: ma and la hold R * S floats each, rowst 64 floats, red
+// nsg * R * D / 4 f32x4 (at most 16 KiB: nsg * R * D / 4 <= max(256, R * D / 4)).
 template <int DT>
-__device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int t, char* smem) {
+__device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int t, float* ma, float* la,
+                               float* rowst, f32x4* red) {
   using E = Elem<DT>;
   using T = typename E::T;
   constexpr int D = kDecD, NDP = D / 4;
@@ -83,11 +88,9 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
   const int r0 = 32 * rb;
   const int R = min(32, dm.G * dm.Sq - r0);
   const int lane = t & 63, wave = t >> 6;
-  float* ma = reinterpret_cast<float*>(smem);  // [R][S]: m, then the scale factors a
-  float* la = ma + R * S;                      // [R][S]: l
-  float* mst = la + R * S;                     // [32]: m* per row
-  float* lst = mst + 32;                       // [32]: l* per row
-  f32x4* red = reinterpret_cast<f32x4*>(smem + (((2 * R * S + 64) * 4 + 15) & ~15));
+  // ma [R][S]: m, then the scale factors a; la [R][S]: l.
+  float* mst = rowst;       // [32]: m* per row
+  float* lst = rowst + 32;  // [32]: l* per row
 
   auto row_index = [&](int rl) -> int64_t {  // workspace row of split 0
     const int r = r0 + rl;
@@ -227,9 +230,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int NI = ST::NI;   // LDS-DMA instructions per wave per K (or V) tile
   // Four separate arrays (K and V of two stages), not one: the compiler can
   // then tell the LDS-DMA target of the tile in flight from the stage being
-  // read and does not wait for those loads before the reads.  The combine
-  // reuses all four as one 64 KiB area (the compiler lays them out in name
-  // order, back to back).
+  // read and does not wait for those loads before the reads.  The fused
+  // combine reuses them, each region inside one array (m and l of up to
+  // kFusedMaxRowSplitsHost (row, split) pairs take one 16 KiB array each).
   __shared__ __attribute__((aligned(1024))) char lds_a_k0[kDecTileBytes];
   __shared__ __attribute__((aligned(1024))) char lds_b_v0[kDecTileBytes];
   __shared__ __attribute__((aligned(1024))) char lds_c_k1[kDecTileBytes];
@@ -586,7 +589,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll 1
   for (int rbc = RW * rbw; rbc < RW * rbw + RW && rbc < p.n_rblk && (32 * rbc) / dm.G < sq; ++rbc) {
     if (rbc > RW * rbw) __syncthreads();  // the previous combine's LDS reads are done
-    decode_combine<DT>(p, b, kvh, rbc, t, lds_a_k0);
+    decode_combine<DT>(p, b, kvh, rbc, t, reinterpret_cast<float*>(lds_a_k0), reinterpret_cast<float*>(lds_b_v0),
+                       reinterpret_cast<float*>(lds_d_v1), reinterpret_cast<f32x4*>(lds_c_k1));
   }
 }
 

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import math
 import threading
+import warnings
 
 import torch
 
@@ -64,7 +65,21 @@ def _workspace_buffer(device: torch.device, stream: int, nbytes: int) -> torch.T
         return buf
 
 
+# Counter buffers of calls made while a graph was being captured: each such
+# call gets its own (replays of two graphs may run concurrently on different
+# streams, so they must not count in one shared buffer), and keeps it for the
+# life of the process, as the graph replays into it.
+_captured: list = []
+
+
 def _counter_buffer(device: torch.device, stream: int, n: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        # Zeroed by a fill kernel recorded in the graph (not a memset node),
+        # so every replay also starts from zero counters.
+        buf = torch.zeros(max(n, 1), dtype=torch.int32, device=device)
+        with _counters_lock:
+            _captured.append(buf)
+        return buf
     key = (device.index, stream)
     with _counters_lock:
         buf = _counters.get(key)
@@ -95,6 +110,44 @@ def workspace_bytes(batch: int, num_heads: int, seq_q: int, head_dim: int, split
 _SCALE_LOG2 = {64: 64 ** -0.5 * LOG2E, 128: 128 ** -0.5 * LOG2E}
 
 
+# The torch-tensor binding of the decode call, once loaded, or the reason it
+# could not be (then every decode step takes the ctypes entry point).
+_host_failed: list = []
+
+
+def _decode_host():
+    """The _gqa_host.so module, or None when it cannot be loaded (missing,
+    stale, or built against another torch or library ABI): a warning is
+    given once and decode_forward calls gqa_split_launch through ctypes —
+    the same C entry point, with more host time per step."""
+    if _lib._host is not None:
+        return _lib._host
+    if _host_failed:
+        return None
+    try:
+        return _lib.load_host()
+    except (RuntimeError, ImportError, OSError) as e:
+        _host_failed.append(repr(e))
+        warnings.warn(f"gqa_kernels: torch-tensor decode binding unavailable ({e}); "
+                      "decode steps call gqa_split_launch through ctypes", RuntimeWarning, stacklevel=3)
+        return None
+
+
+def _split_launch_ctypes(q, k, v, ws, splits, causal, scale_log2, return_lse, stream):
+    """gqa_split_launch through ctypes into a fresh o (and lse)."""
+    lib = _lib.load()
+    batch, num_heads, seq_q, head_dim = q.shape
+    _, num_kv_heads, seq_kv, _ = k.shape
+    o = torch.empty_like(q)
+    lse = torch.empty(batch, num_heads, seq_q, dtype=torch.float32, device=q.device) if return_lse else None
+    _lib.check(lib.gqa_split_launch(
+        q.data_ptr(), _lib.strides(q), k.data_ptr(), _lib.strides(k), v.data_ptr(), _lib.strides(v),
+        o.data_ptr(), _lib.strides(o), None if lse is None else lse.data_ptr(), ws.data_ptr(), splits,
+        batch, num_heads, num_kv_heads, seq_q, seq_kv, head_dim, scale_log2, int(bool(causal)),
+        _DTYPES[q.dtype], stream))
+    return o if lse is None else (o, lse)
+
+
 def decode_forward(q, k, v, causal, splits, return_lse, dev):
     """The two-launch split-KV forward as gqa_flash_attn takes it: kernel-ready
     q, k, v on device index `dev` (the current device), the stream's cached
@@ -109,7 +162,9 @@ def decode_forward(q, k, v, causal, splits, return_lse, dev):
         ws = _workspace_buffer(q.device, stream, need)
     # gqa_split_launch through the torch-tensor binding (_gqa_host.so): the
     # argument marshalling of a decode step in C++ rather than ctypes.
-    host = _lib._host if _lib._host is not None else _lib.load_host()
+    host = _lib._host if _lib._host is not None else _decode_host()
+    if host is None:
+        return _split_launch_ctypes(q, k, v, ws, splits, causal, _SCALE_LOG2[head_dim], return_lse, stream)
     return host.split_decode(q, k, v, ws, splits, bool(causal), _SCALE_LOG2[head_dim], _DTYPES[q.dtype],
                              bool(return_lse))
 

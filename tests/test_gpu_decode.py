@@ -100,3 +100,25 @@ def test_decode_wide_row_blocks_route_and_repeatability():
         assert torch.equal(gqa_flash_attn(q, k, v, causal=True), o)
     torch.cuda.synchronize()
     assert_close(o, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], "verify step")
+
+
+@pytest.mark.parametrize("Hq,Hkv,sq,skv,S", [
+    (32, 4, 4, 128 * 64 + 37, 128),  # G * Sq = 32 valid rows x 128 splits: R * S = 4096, the fused limit
+    (64, 8, 4, 64 * 64, 64),         # the 70B group, 32 rows x 64 splits
+])
+def test_decode_fused_combine_at_its_lds_limit(Hq, Hkv, sq, skv, S):
+    # The fused combine stages m and l of R valid rows x S splits in LDS; at
+    # R * S = 4096 they fill their 16 KiB stage arrays.  It must agree with
+    # the two-launch combine (same partials, same arithmetic) and the oracle.
+    from gqa_kernels.gqa_split import FUSED_MAX_ROW_SPLITS, split_kv_forward
+    assert min(32, Hq // Hkv * sq) * S <= FUSED_MAX_ROW_SPLITS
+    q, k, v = make_inputs(1, Hq, Hkv, sq, skv, 128, torch.bfloat16, seed=S + sq, device=DEV)
+    print(f"fused combine limit Hq={Hq} Hkv={Hkv} sq={sq} skv={skv} S={S}", flush=True)
+    o2, lse2 = split_kv_forward(q, k, v, True, S, fused=False, return_lse=True)
+    of, lsef = split_kv_forward(q, k, v, True, S, fused=True, return_lse=True)
+    torch.cuda.synchronize()
+    # Same partials, combined in a different order: the outputs differ by at
+    # most a bf16 rounding step of |o| < 1 (2^-8).
+    assert (of.float() - o2.float()).abs().max().item() <= 2 ** -8, "fused and two-launch combines differ"
+    assert torch.allclose(lsef, lse2, rtol=0, atol=1e-4)
+    assert_close(of, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], f"fused S={S}")

@@ -143,3 +143,28 @@ def test_paged_decode_in_graph():
     expect = fn().clone()
     g, out = _capture(fn)
     _replays(g, out, expect)
+
+
+@pytest.mark.parametrize("shape", [(4, 32, 8, 4096, 4096),   # 2048 items: the dynamic schedule's queues
+                                   (1, 32, 8, 1024, 1024)])  # key-split blocks: the merge counters
+def test_two_graphs_replayed_concurrently(shape):
+    # Two prefills captured into two graphs (on torch's one capture stream),
+    # then replayed at the same time on two streams: each captured call has
+    # its own counters (queue and merge counters that the kernel leaves
+    # zero), so neither replay sees the other's claims.
+    from gqa_kernels import gqa_flash_attn
+    b, hq, hkv, sq, skv = shape
+    print(f"two graphs concurrently {shape}", flush=True)
+    ins = [make_inputs(b, hq, hkv, sq, skv, 128, torch.bfloat16, seed=s, device=DEV) for s in (1, 2)]
+    expect = [gqa_flash_attn(*x, causal=True) for x in ins]
+    graphs = [_capture(lambda x=x: gqa_flash_attn(*x, causal=True)) for x in ins]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(4):
+        torch.cuda.synchronize()
+        for (g, _), st in zip(graphs, streams):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                g.replay()
+        torch.cuda.synchronize()
+        for i, ((_, out), e) in enumerate(zip(graphs, expect)):
+            assert torch.equal(out, e), f"replay {rep} of graph {i} differs from the eager result"

@@ -73,6 +73,48 @@ def test_host_binding_loads(lib):
     assert _lib.load_host() is host
 
 
+def test_decode_falls_back_to_ctypes_without_host_binding(monkeypatch):
+    """A decode step whose torch-tensor binding cannot be loaded (missing,
+    stale, or built against another torch) still runs: decode_forward warns
+    once and calls gqa_split_launch through ctypes with the same arguments
+    (the C call is replaced by a recorder here: no GPU)."""
+    from gqa_kernels import _lib, gqa_split
+
+    calls = []
+
+    class _Stub:
+        def gqa_split_launch(self, *args):
+            calls.append(args)
+            return 0
+
+    def _no_host():
+        raise ImportError("undefined symbol: _ZN3c10 (built against another torch)")
+
+    monkeypatch.setattr(_lib, "_host", None)
+    monkeypatch.setattr(_lib, "load_host", _no_host)
+    monkeypatch.setattr(_lib, "load", lambda: _Stub())
+    monkeypatch.setattr(gqa_split, "_host_failed", [])
+    monkeypatch.setattr(gqa_split, "_workspaces", {})
+    monkeypatch.setattr(gqa_split, "_raw_stream", lambda dev: 1234)
+    q = torch.zeros(1, 32, 1, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 8, 4096, 128, dtype=torch.bfloat16)
+    v = torch.zeros_like(k)
+    with pytest.warns(RuntimeWarning, match="ctypes"):
+        o = gqa_split.decode_forward(q, k, v, True, 16, False, 0)
+    assert o.shape == q.shape and o.dtype == q.dtype
+    o2, lse = gqa_split.decode_forward(q, k, v, True, 16, True, 0)  # no second warning needed
+    assert lse.shape == (1, 32, 1) and lse.dtype == torch.float32
+    assert len(calls) == 2
+    a = calls[0]
+    # q, o pointers; splits; B, Hq, Hkv, Sq, Skv, D; scale; causal; dtype; stream
+    assert a[0] == q.data_ptr() and a[6] == o.data_ptr() and a[8] is None
+    assert a[10:17] == (16, 1, 32, 8, 1, 4096, 128)
+    assert abs(a[17] - 128 ** -0.5 * 1.4426950408889634) < 1e-7
+    assert a[18:] == (1, _lib.DTYPE_BF16, 1234)
+    assert calls[1][8] == lse.data_ptr()
+    assert len(gqa_split._host_failed) == 1
+
+
 def test_workspace_bytes(lib):
     from gqa_kernels.gqa_split import workspace_bytes
     for args in ((1, 32, 1, 128, 128), (16, 64, 4, 128, 8), (2, 8, 3, 64, 7)):
