@@ -12,6 +12,12 @@
 // layout of S^T is already the B-operand layout P^T needs for the second
 // product (no register shuffle between the two MFMA chains).
 //
+// v_mfma_f32_16x16x32_{bf16,f16} (Elem::mfma16, the 16-row decode pass),
+// confirmed on the MI355X with a one-wave probe:
+//   A operand (16 x 32, M x K): lane l holds A[l % 16][8*(l/16) + e], e = 0..7
+//   B operand (32 x 16, K x N): lane l holds B[8*(l/16) + e][l % 16]
+//   C/D       (16 x 16)       : lane l, register v holds C[4*(l/16) + v][l % 16]
+//
 // Key order inside a 32-key block: the M index m of S^T is mapped to key
 // pi(m) = m with bits 2 and 3 swapped.  With that map, register v of the
 // S^T accumulator in lane l holds key 16*(v/8) + 8*(l/32) + (v%8), so the 8
@@ -44,6 +50,11 @@ template <> struct Elem<0> {  // bf16
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // v_mfma_f32_16x16x32_bf16 (layout in the header comment).
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
   // Round-to-nearest-even conversion of two floats, packed lo | hi << 16.
   __device__ static inline uint32_t pack2(float lo, float hi) {
     typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
@@ -58,6 +69,10 @@ template <> struct Elem<1> {  // fp16
   using T = _Float16;
   __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float lo, float hi) {
@@ -92,6 +107,16 @@ __device__ inline float xhalf_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The same for lane (l ^ 16): v_permlane16_swap exchanges the odd 16-lane
+// rows of its first operand with the even rows of its second.
+__device__ inline float xquad_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xquad_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------

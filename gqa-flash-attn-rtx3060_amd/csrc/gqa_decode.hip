@@ -594,6 +594,319 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ---------------------------------------------------------------------------
+// 16-row first pass: a (b, kv head) with at most 16 packed rows (a decode
+// step of one token up to G = 16, or of 16 / G tokens).  Same stream, tile
+// order, partials and combine as gqa_decode_kernel, with the tile computed
+// by v_mfma_f32_16x16x32: half the matrix cycles, and half the scores per
+// lane (16 instead of 32, with 28 of every 32 rows of the 32-row form being
+// padding at a Llama-3.1-8B decode step), so a chunk's tiles take about
+// half the compute between their arrival and the next refill.  At these
+// shapes the time between a tile's arrival and the issue of its stage's
+// next tile is what bounds each workgroup's stream (decode at 2K-32K keys
+// runs as fast from the Infinity Cache as from HBM).
+//
+// Lane l = (row i16 = l % 16, lane group lg = l / 16).  S^T for the 64 keys
+// of a tile is four 16-key blocks: register v of block kb holds key
+// 16 kb + 4 lg + v of row i16 (C layout of the 16x16 MFMA), so a row's 64
+// scores are spread over the 4 lane groups (row max / sum across them by
+// v_permlane16_swap and v_permlane32_swap).  The P^T operand of the 32-key
+// block j takes lane l's own 8 probabilities — keys 32 j + 4 lg + 0..3 and
+// 32 j + 16 + 4 lg + 0..3 — as k-slots 8 lg + 0..7, so the V^T operand reads
+// the same two 4-key runs (two ds_read_b64_tr_b16).  V tiles are swizzled
+// by sv16(r) = 2 (r & 7): the 8 rows one half-wave's transposing read
+// touches (two lane groups x 4 keys) then cover all 64 banks once.  Wave w
+// accumulates O^T for dims [32 w, 32 w + 32) as two 16-dim blocks.
+// ---------------------------------------------------------------------------
+template <int DT, int KV>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_decode16_kernel(SplitParams p) {
+  constexpr int D = kDecD;
+  constexpr bool PAGED = KV != 0;
+  using E = Elem<DT>;
+  using ST = FwdStage<D>;
+  constexpr int CPR = ST::CPR;
+  constexpr int NI = ST::NI;    // LDS-DMA instructions per wave per K (or V) tile
+  constexpr int NKS = D / 32;   // k-steps of S^T
+  // LDS as gqa_decode_kernel: two stages (64 KiB, two workgroups per CU;
+  // a third stage for grids of one workgroup per CU measured slower at 8K-32K
+  // keys), reused by the fused combine.
+  __shared__ __attribute__((aligned(1024))) char lds_a_k0[kDecTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b_v0[kDecTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_c_k1[kDecTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_d_v1[kDecTileBytes];
+  __shared__ int s_last;
+
+  const Dims& dm = p.dm;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;
+  const int i16 = lane & 15, lg = lane >> 4;
+
+  const int total = dm.B * dm.Hkv * p.splits;  // one row block per (b, kv head)
+  const int w = xcd_remap(blockIdx.x, total);
+  const int s = w % p.splits;
+  const int rest = w / p.splits;
+  const int kvh = rest % dm.Hkv;
+  const int b = rest / dm.Hkv;
+  const int skv = PAGED ? min(max(load_uniform(p.seq_lens + b), 0), dm.Skv) : dm.Skv;
+  const bool varlen = p.q_len != nullptr;
+  const int sq = varlen ? min(max(load_uniform(p.q_len + b), 0), dm.Sq) : dm.Sq;
+  const int64_t tok0 = varlen ? (int64_t)load_uniform(p.q_start + b) : 0;
+  if (sq <= 0) return;  // a sequence without query rows (variable lengths)
+
+  // This lane's query row (position-major packing).
+  const int pos = i16 / dm.G, g = i16 - pos * dm.G;
+  const bool valid = pos < sq;
+  const int head = kvh * dm.G + g;
+  const int qpos = pos + (skv - sq);
+
+  // Keys of this chunk (gqa_split.py:55-60), clamped to the block's last
+  // visible key under causal.
+  const int c0 = s * p.chunk;
+  int c1 = min(c0 + p.chunk, skv);
+  const int pos_hi = min(sq - 1, 15 / dm.G);
+  if (dm.causal) c1 = min(c1, pos_hi + (skv - sq) + 1);
+  const int nk = max(c1 - c0, 0);
+  const int ntiles = (nk + 63) >> 6;
+  const int qpos_lo = skv - sq;
+
+  const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
+  const char* kbase = static_cast<const char*>(p.k.ptr) +
+                      2 * ((PAGED ? 0 : (int64_t)b * p.k.sb + (int64_t)c0 * p.k.ss) + (int64_t)kvh * p.k.sh);
+  const char* vbase = static_cast<const char*>(p.v.ptr) +
+                      2 * ((PAGED ? 0 : (int64_t)b * p.v.sb + (int64_t)c0 * p.v.ss) + (int64_t)kvh * p.v.sh);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, !PAGED && nk > 0 ? (uint32_t)(nk - 1) * kssb + 2 * D : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, !PAGED && nk > 0 ? (uint32_t)(nk - 1) * vssb + 2 * D : 0u);
+  const int* table_row = PAGED ? p.block_table + (int64_t)b * p.table_stride : nullptr;
+
+  // Tile order: splits start a quarter of the chunk apart (as gqa_decode_kernel).
+  const int rot = (p.rotate && ntiles >= 4) ? (s & 3) * (ntiles >> 2) : 0;
+  auto tile_rel = [&](int it) {
+    const int j = it + rot;
+    return it >= ntiles ? it : (j >= ntiles ? j - ntiles : j);
+  };
+
+  // LDS-DMA source offsets of this lane: its row within an instruction's 4
+  // rows, its chunk swizzled by gk (K) or sv16 (V) of the tile row, whose
+  // low three bits are 4 (wave & 1) + lrow for every instruction this wave
+  // issues (instruction j of wave w loads rows 16 j + 4 w + 0..3).
+  const int lrow = lane / CPR;
+  const uint32_t koff =
+      (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ ST::gk((wave * ST::RPI + lrow) & 15));
+  const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ (2 * ((4 * (wave & 1) + lrow) & 7)));
+  auto issue = [&](int it, char* kst, char* vst) {
+    const int j = tile_rel(it) * 64;
+    if constexpr (KV == 0) {
+      issue_tile_dma<D, kDmaStream>(kst, rk, (uint32_t)j * kssb, kssb, koff, wave);
+      issue_tile_dma<D, kDmaStream>(vst, rv, (uint32_t)j * vssb, vssb, voff, wave);
+    } else if constexpr (KV == 1) {
+      const int key0 = c0 + j, rows = c1 - key0;
+      __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
+      if (rows > 0) {
+        const int64_t pg = load_uniform(table_row + (key0 >> p.block_shift));
+        const int64_t slot = key0 & ((1 << p.block_shift) - 1);
+        const uint32_t n = (uint32_t)(min(rows, 64) - 1);
+        tk = make_rsrc(kbase + 2 * (pg * p.k.sb + slot * p.k.ss), n * kssb + 2 * D);
+        tv = make_rsrc(vbase + 2 * (pg * p.v.sb + slot * p.v.ss), n * vssb + 2 * D);
+      }
+      issue_tile_dma<D, kDmaStream>(kst, tk, 0u, kssb, koff, wave);
+      issue_tile_dma<D, kDmaStream>(vst, tv, 0u, vssb, voff, wave);
+    } else {
+      typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+      for (int jj = 0; jj < NI; ++jj) {
+        const int step = jj * 4 + wave;
+        const int key = c0 + j + step * ST::RPI, rows = c1 - key;
+        __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
+        if (rows > 0) {
+          const int64_t pg = load_uniform(table_row + (key >> p.block_shift));
+          const int64_t slot = key & ((1 << p.block_shift) - 1);
+          const uint32_t n = (uint32_t)(min(rows, ST::RPI) - 1);
+          tk = make_rsrc(kbase + 2 * (pg * p.k.sb + slot * p.k.ss), n * kssb + 2 * D);
+          tv = make_rsrc(vbase + 2 * (pg * p.v.sb + slot * p.v.ss), n * vssb + 2 * D);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tk, (lds_void*)(kst + step * 1024), 16, koff, 0, 0, kDmaStream);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tv, (lds_void*)(vst + step * 1024), 16, voff, 0, 0, kDmaStream);
+      }
+    }
+  };
+
+  // Loads in issue order: tile 0, Q (only lanes of valid rows touch memory:
+  // an invalid lane's offset lies past the query group's descriptor and
+  // reads zero), tile 1.
+  issue(0, lds_a_k0, lds_b_v0);
+  u32x4 qreg[NKS];
+  {
+    const char* qg = static_cast<const char*>(p.q.ptr) +
+                     2 * ((varlen ? tok0 * p.q.ss : (int64_t)b * p.q.sb) + (int64_t)kvh * dm.G * p.q.sh);
+    const uint32_t qext = (uint32_t)(2 * ((int64_t)(dm.G - 1) * p.q.sh + (int64_t)(sq - 1) * p.q.ss + D));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(qg, qext);
+    const uint32_t qo = valid ? (uint32_t)(2 * ((int64_t)g * p.q.sh + (int64_t)pos * p.q.ss) + 16 * lg) : 0x80000000u;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      qreg[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 64u * ks, 0, 0));
+  }
+  issue(1, lds_c_k1, lds_d_v1);
+  // Tile 0 and Q have landed (tile 1 may still be in flight).
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NI));
+
+  // LDS read offsets.  K: row 16 kb + i16, chunk 4 ks + lg (16 lanes of a
+  // lane group read 16 rows at distinct swizzled chunks: conflict-free).
+  // V: the first run's row 4 lg + jj / 4 (jj = lane within its 16-lane
+  // group), dims 32 wave + 16 db + 4 (jj % 4).
+  uint32_t ka[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) ka[ks] = (uint32_t)(i16 * (2 * D) + 16 * ((4 * ks + lg) ^ ST::gk(i16))) & 0xFF0u;
+  uint32_t vb[2];
+  {
+    const int jj = lane & 15;
+    const int rr = 4 * lg + (jj >> 2);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+      vb[db] = (uint32_t)(rr * (2 * D) + 16 * ((4 * wave + 2 * db + ((jj & 3) >> 1)) ^ (2 * (rr & 7))) + 8 * (jj & 1)) &
+               0xFF8u;
+  }
+
+  f32x4 acc[2] = {};
+  float m_run = -__builtin_inff(), l_run = 0.f;
+  const float c = dm.c;
+
+  auto set_prio = [&](int it) {
+    const int lvl = (4 * it) / ntiles;
+    if (lvl == 0) __builtin_amdgcn_s_setprio(3);
+    else if (lvl == 1) __builtin_amdgcn_s_setprio(2);
+    else if (lvl == 2) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+  };
+
+  auto step = [&](auto s3, auto issue_c, auto last_c, int it) {
+    constexpr int S3 = decltype(s3)::value;
+    constexpr bool ISSUE = decltype(issue_c)::value;
+    constexpr bool LAST = decltype(last_c)::value;
+    char* kst = S3 == 0 ? lds_a_k0 : lds_c_k1;
+    char* vst = S3 == 0 ? lds_b_v0 : lds_d_v1;
+    const char* ck = kst;
+    const char* cv = vst;
+    if ((it & 3) == 0) set_prio(it);
+    // This wave's loads of tile it have landed (those of tile it + 1 may
+    // still be in flight); after the barrier, every wave's have.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LAST ? 0 : 2 * NI));
+    phase_barrier();
+
+    // S^T for the 64 keys: four 16-key blocks, NKS k-steps each.
+    f32x4 sc[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
+    {
+      u32x4 opk[4 * NKS];
+#pragma unroll
+      for (int j = 0; j < 4 * NKS; ++j)
+        opk[j] = *reinterpret_cast<const u32x4*>(ck + (j / NKS) * 16 * (2 * D) + ka[j % NKS]);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) sc[kb] = E::mfma16(opk[kb * NKS + ks], qreg[ks], sc[kb]);
+    }
+    const int key0 = c0 + tile_rel(it) * 64;
+    const bool need_mask = (key0 + 64 > c1) || (dm.causal && key0 + 63 > qpos_lo);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int key = key0 + 16 * kb + 4 * lg + v;
+          const bool off = key >= c1 || (dm.causal && key > qpos);
+          sc[kb][v] = off ? -__builtin_inff() : sc[kb][v];
+        }
+    }
+    // Exact online softmax (gqa_split.py:92-101) in exp2 units; a row with
+    // no visible key so far keeps m = -inf and uses 0 as reference.
+    const float t0 = vmax3(sc[0][0], sc[0][1], sc[0][2]), t1 = vmax3(sc[0][3], sc[1][0], sc[1][1]);
+    const float t2 = vmax3(sc[1][2], sc[1][3], sc[2][0]), t3 = vmax3(sc[2][1], sc[2][2], sc[2][3]);
+    const float t4 = vmax3(sc[3][0], sc[3][1], sc[3][2]);
+    const float mx = xhalf_max(xquad_max(fmaxf(vmax3(t0, t1, t2), vmax3(t3, t4, sc[3][3]))));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = fast_exp2((m_run - m_use) * c);
+    const float nmc = -m_use * c;
+    float pv[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) pv[kb][v] = fast_exp2(__builtin_fmaf(sc[kb][v], c, nmc));
+    const float rs = ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) + ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3])) +
+                     (((pv[2][0] + pv[2][1]) + (pv[2][2] + pv[2][3])) + ((pv[3][0] + pv[3][1]) + (pv[3][2] + pv[3][3])));
+    u32x4 pk[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      pk[j] = u32x4{E::pack2(pv[2 * j][0], pv[2 * j][1]), E::pack2(pv[2 * j][2], pv[2 * j][3]),
+                    E::pack2(pv[2 * j + 1][0], pv[2 * j + 1][1]), E::pack2(pv[2 * j + 1][2], pv[2 * j + 1][3])};
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 2; ++db) acc[db] *= alpha;
+
+    // O^T (this wave's dims) += V^T P^T over the 64 keys.
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const u32x2 lo = ld_tr(cv + vb[db] + (32 * j) * (2 * D));
+        const u32x2 hi = ld_tr(cv + vb[db] + (32 * j + 16) * (2 * D));
+        acc[db] = E::mfma16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[j], acc[db]);
+      }
+    phase_barrier();
+    if constexpr (ISSUE) issue(it + 2, kst, vst);
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using BT = std::true_type;
+  using BF = std::false_type;
+  // Tiles in pairs; an odd count is padded with one tile past the chunk
+  // (zeros, every key masked); the last pair refills nothing.
+  const int ne = (ntiles + 1) & ~1;
+  int it = 0;
+  for (; it + 4 <= ne; it += 2) {
+    step(I0{}, BT{}, BF{}, it);
+    step(I1{}, BT{}, BF{}, it + 1);
+  }
+  if (it < ne) {
+    step(I0{}, BF{}, BF{}, it);
+    step(I1{}, BF{}, BT{}, it + 1);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // This wave's dims of the valid rows' partials: lane (i16, lg) holds dims
+  // 32 wave + 16 db + 4 lg + 0..3 in acc[db]; l is summed over the 4 lane
+  // groups (each holds the sum over its own keys).
+  const float l_tot = xhalf_sum(xquad_sum(l_run));
+  if (valid) {
+    const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+      store_coherent4(rw, (uint32_t)((row * D + 32 * wave + 16 * db + 4 * lg) * 4), acc[db]);
+    if (wave == 0 && lg == 0) {
+      store_coherent(p.ws_m + row, skv == 0 ? 0.f : m_run * c);
+      store_coherent(p.ws_l + row, l_tot);
+    }
+  }
+
+  if (PAGED || p.counters == nullptr) return;
+  // Fused combine, as gqa_decode_kernel.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const int idx = (b * dm.Hkv + kvh) * p.n_rblk;
+    const int prev = __hip_atomic_fetch_add(&p.counters[idx], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == p.splits - 1);
+    if (s_last) __hip_atomic_store(&p.counters[idx], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  decode_combine<DT>(p, b, kvh, 0, t, reinterpret_cast<float*>(lds_a_k0), reinterpret_cast<float*>(lds_b_v0),
+                     reinterpret_cast<float*>(lds_d_v1), reinterpret_cast<f32x4*>(lds_c_k1));
+}
+
 bool decode_kernel_fits(const SplitParams& p) {
   if (p.dm.D != kDecD) return false;
   const bool paged = p.block_table != nullptr;
@@ -617,7 +930,9 @@ static hipError_t launch_decode_t(const SplitParams& p, hipStream_t stream) {
   const int rw = p.n_rblk >= 3 ? 4 : p.n_rblk == 2 ? 2 : 1;
   const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * ((p.n_rblk + rw - 1) / rw) * p.splits;
   if (total <= 0) return hipSuccess;
-  if (rw == 4)
+  if (p.dm.G * p.dm.Sq <= 16)
+    hipLaunchKernelGGL((gqa_decode16_kernel<DT, KV>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  else if (rw == 4)
     hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 4>), dim3((unsigned)total), dim3(256), 0, stream, p);
   else if (rw == 2)
     hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 2>), dim3((unsigned)total), dim3(256), 0, stream, p);

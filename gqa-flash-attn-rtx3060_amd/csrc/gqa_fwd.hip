@@ -869,19 +869,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   }
 }
 
-// Compute units of the current device (one persistent workgroup each),
-// cached per device.
-static int device_cu_count() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cached[dev] = n;
-  return n;
-}
-
 template <int DT, int D, int PG>
 static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
   const int per_bh = (PG == 0 && p.kv_splits > 0) ? p.n_mblk * p.kv_splits : p.n_mblk + p.n_split;

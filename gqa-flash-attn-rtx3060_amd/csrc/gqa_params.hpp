@@ -149,6 +149,18 @@ struct CacheWriteParams {
   int elem_bytes;
 };
 
+// Compute units of the current device (0 if unknown), cached per device.
+inline int device_cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
 hipError_t launch_fwd(const FwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_split_first(const SplitParams& p, int dtype, hipStream_t stream);  // fused if p.counters
