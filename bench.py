@@ -287,6 +287,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline legs")
+    ap.add_argument("--warm-ms", type=float, default=WARM_MS,
+                    help="minimum untimed time per config beyond the headline (0: the --warmup calls only; "
+                         "for counter-collection runs)")
     ap.add_argument("--config", default=None,
                     help="with --only configs: time only the BASELINE configs whose name starts with this")
     ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b", "configs",
@@ -299,6 +302,7 @@ def main() -> int:
                          "'extras' the verify-step and key-chunk shapes")
     args = ap.parse_args()
 
+    _set_warm_ms(args.warm_ms)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
@@ -518,6 +522,11 @@ EXTRAS = (
 # GPU idle meanwhile, and the clock needs tens of milliseconds of load to
 # ramp back up).
 WARM_MS = 150.0
+
+
+def _set_warm_ms(ms: float) -> None:
+    global WARM_MS
+    WARM_MS = ms
 # K/V sets rotated per HBM-bound config: enough that consecutive calls cannot
 # find the previous calls' keys in the 256 MB Infinity Cache.
 ROTATE_BYTES = 600e6

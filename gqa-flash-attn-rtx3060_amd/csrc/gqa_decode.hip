@@ -398,7 +398,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint32_t ka[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
-    ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
+    ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ ST::gk(pi_key(i)))) & kKMask;
   uint32_t vb[NDB];
   {
     const int q = lane >> 4, ii = lane & 15;

@@ -402,7 +402,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   uint32_t ka[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
-    ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ (i & (CPR - 1)))) & kKMask;
+    ka[ks] = (uint32_t)(pi_key(i) * (2 * D) + 16 * ((2 * ks + hh) ^ ST::gk(pi_key(i)))) & kKMask;
   // At D = 128, K stages 1 and 2 lie above 64 KiB, out of reach of
   // ds_read's 16-bit offset field.  Their reads address from kah = ka + the
   // LDS address of stage 1, kept in registers (refreshed as opaque values in

@@ -17,8 +17,8 @@ namespace gqa {
 // fetches chunk pc ^ swizzle(r).
 //
 // K: gk is chosen so that the S^T A-operand reads (row pi(i), chunk 2ks+h)
-// hit distinct bank groups in every 16 consecutive lanes; with it,
-// gk(pi(i)) = i & (CPR - 1), so the chunk lane i reads is (2ks+h) ^ i.
+// hit distinct bank groups in every 16 consecutive lanes; the chunk lane i
+// reads is (2ks+h) ^ gk(pi(i)).
 //
 // V: read transposed by ds_read_b64_tr_b16.  In each 16-lane group of such a
 // read, lane j addresses V[r0 + j/4][d0 + 4*(j%4)] and receives
@@ -34,9 +34,12 @@ template <int D> struct FwdStage {
   static constexpr int RPI = 64 / CPR;              // rows per LDS-DMA instruction
   static constexpr int NI = (kKeys * CPR) / 256;    // LDS-DMA instructions per wave of a group
 
+  // D = 128 (256-byte rows): gk(pi(i)) = i & 15.  D = 64 (128-byte rows,
+  // bank group 8 (r & 1) + chunk): gk(pi(i)) = (i >> 1) & 7, so the 16 lanes
+  // of a 128-bit read (rows pi(0..15)) hit 16 distinct bank groups.
   __device__ static constexpr int gk(int r) {
     return CPR == 16 ? ((r & 3) | (((r >> 3) & 1) << 2) | (((r >> 2) & 1) << 3))
-                     : ((r & 3) | (((r >> 3) & 1) << 2));
+                     : (((r >> 1) & 1) | (((r >> 3) & 1) << 1) | (((r >> 2) & 1) << 2));
   }
   __device__ static constexpr int sv(int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 };
