@@ -211,9 +211,11 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
 }  // namespace
 
 // KV: 0 contiguous K/V; 1 a paged cache with pages of >= 64 keys (one
-// buffer descriptor per 64-key tile, from the block table); 2 pages of 4-32
-// keys (one descriptor per LDS-DMA instruction, whose 4 rows lie in one
-// page).  Paged caches are (num_blocks, block_size, Hkv, D) in any strides
+// buffer descriptor per 64-key tile, from the block table); 3 pages of
+// 16-32 keys (one descriptor per wave and tile: each wave loads 16
+// consecutive rows); 2 pages of 4-8 keys (one descriptor per LDS-DMA
+// instruction, whose 4 rows lie in one page).  Paged caches are
+// (num_blocks, block_size, Hkv, D) in any strides
 // (SplitParams::k/v: sb = block, ss = slot, sh = head stride); sequence b has
 // min(seq_lens[b], Skv) keys.  With q_start / q_len set, q is token-major and
 // sequence b has q_len[b] query rows from token q_start[b].
@@ -344,8 +346,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       issue_tile_dma<D, kDmaStream>(kst, tk, 0u, kssb, koff, wave);
       issue_tile_dma<D, kDmaStream>(vst, tv, 0u, vssb, voff, wave);
+    } else if constexpr (KV == 3) {
+      // Pages of 16-32 keys: this wave loads rows [key, key + 16) of the
+      // tile, one run in one page (one table read, one descriptor each for K
+      // and V); instruction jj takes rows key + 4 jj + 0..3 (scalar offset)
+      // into LDS rows 16 wave + 4 jj + ...  K's swizzle is linear in the row
+      // bits: chunk (lane % CPR) ^ gk(lrow) ^ gk(4 jj); V's depends on lrow.
+      typedef __attribute__((address_space(3))) void lds_void;
+      const int key = c0 + j + 16 * wave, rows = c1 - key;
+      __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
+      if (rows > 0) {
+        const int64_t pg = load_uniform(table_row + (key >> p.block_shift));
+        const int64_t slot = key & ((1 << p.block_shift) - 1);
+        const uint32_t n = (uint32_t)(min(rows, 16) - 1);
+        tk = make_rsrc(kbase + 2 * (pg * p.k.sb + slot * p.k.ss), n * kssb + 2 * D);
+        tv = make_rsrc(vbase + 2 * (pg * p.v.sb + slot * p.v.ss), n * vssb + 2 * D);
+      }
+#pragma unroll
+      for (int jj = 0; jj < NI; ++jj) {
+        const uint32_t ko = (uint32_t)(lrow * kssb) +
+                            16u * (uint32_t)((lane % CPR) ^ ST::gk(lrow) ^ ST::gk(jj * ST::RPI));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tk, (lds_void*)(kst + (wave * NI + jj) * 1024), 16, ko,
+                                                 (uint32_t)(jj * ST::RPI) * kssb, 0, kDmaStream);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tv, (lds_void*)(vst + (wave * NI + jj) * 1024), 16, voff,
+                                                 (uint32_t)(jj * ST::RPI) * vssb, 0, kDmaStream);
+      }
     } else {
-      // Pages of 4-32 keys: instruction `step` loads rows [key, key + 4) of
+      // Pages of 4-8 keys: instruction `step` loads rows [key, key + 4) of
       // the tile, one run in one page; each gets its own descriptors.
       typedef __attribute__((address_space(3))) void lds_void;
 #pragma unroll
@@ -710,6 +737,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       issue_tile_dma<D, kDmaStream>(kst, tk, 0u, kssb, koff, wave);
       issue_tile_dma<D, kDmaStream>(vst, tv, 0u, vssb, voff, wave);
+    } else if constexpr (KV == 3) {
+      // Pages of 16-32 keys: this wave loads rows [key, key + 16) of the
+      // tile (one page; as gqa_decode_kernel).  The V swizzle sv16 of row
+      // 16 wave + 4 jj + lrow is 2 (4 (jj & 1) + lrow).
+      typedef __attribute__((address_space(3))) void lds_void;
+      const int key = c0 + j + 16 * wave, rows = c1 - key;
+      __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
+      if (rows > 0) {
+        const int64_t pg = load_uniform(table_row + (key >> p.block_shift));
+        const int64_t slot = key & ((1 << p.block_shift) - 1);
+        const uint32_t n = (uint32_t)(min(rows, 16) - 1);
+        tk = make_rsrc(kbase + 2 * (pg * p.k.sb + slot * p.k.ss), n * kssb + 2 * D);
+        tv = make_rsrc(vbase + 2 * (pg * p.v.sb + slot * p.v.ss), n * vssb + 2 * D);
+      }
+#pragma unroll
+      for (int jj = 0; jj < NI; ++jj) {
+        const uint32_t ko = (uint32_t)(lrow * kssb) +
+                            16u * (uint32_t)((lane % CPR) ^ ST::gk(lrow) ^ ST::gk(jj * ST::RPI));
+        const uint32_t vo = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ (2 * (4 * (jj & 1) + lrow)));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tk, (lds_void*)(kst + (wave * NI + jj) * 1024), 16, ko,
+                                                 (uint32_t)(jj * ST::RPI) * kssb, 0, kDmaStream);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(tv, (lds_void*)(vst + (wave * NI + jj) * 1024), 16, vo,
+                                                 (uint32_t)(jj * ST::RPI) * vssb, 0, kDmaStream);
+      }
     } else {
       typedef __attribute__((address_space(3))) void lds_void;
 #pragma unroll
@@ -948,7 +999,8 @@ static hipError_t launch_decode_kv(const SplitParams& p, int dtype, hipStream_t 
 
 hipError_t launch_decode_first(const SplitParams& p, int dtype, hipStream_t stream) {
   if (p.block_table == nullptr) return launch_decode_kv<0>(p, dtype, stream);
-  return p.block_shift >= 6 ? launch_decode_kv<1>(p, dtype, stream) : launch_decode_kv<2>(p, dtype, stream);
+  if (p.block_shift >= 6) return launch_decode_kv<1>(p, dtype, stream);
+  return p.block_shift >= 4 ? launch_decode_kv<3>(p, dtype, stream) : launch_decode_kv<2>(p, dtype, stream);
 }
 
 }  // namespace gqa

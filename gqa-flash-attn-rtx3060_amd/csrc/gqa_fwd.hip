@@ -133,9 +133,11 @@ __device__ __forceinline__ void mphase_pipe() {
 
 // PG: 0 contiguous K/V; 1 a paged cache through the block table with pages
 // of >= 64 keys (one buffer descriptor per 64-key tile, ending at the
-// sequence's last key); 2 pages of RPI..32 keys (RPI = 512 / D rows per
+// sequence's last key); 2 pages of RPI..8 keys (RPI = 512 / D rows per
 // LDS-DMA instruction: each instruction's rows lie in one page, and every
-// instruction gets its own descriptor).
+// instruction gets its own descriptor); 3 pages of 16 or 32 keys (each wave
+// loads 16 consecutive rows of a tile, which lie in one page: one table
+// read and one descriptor per wave and tile).
 // D = 64 keeps to 128 VGPRs (four waves per SIMD): two workgroups share a
 // compute unit, which outweighs the shorter LDS-read lookahead it needs.
 //
@@ -157,6 +159,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   constexpr int CPR = ST::CPR;
   constexpr bool PAGED = PG != 0;
   constexpr bool SMALL = PG == 2;
+  constexpr bool MEDIUM = PG == 3;
   constexpr bool PERSIST = PG == 0 && D == 128;
   // Block ids a wave needs per tile: one, or (small pages) one per LDS-DMA
   // instruction it issues.
@@ -346,15 +349,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
         const int key = key0 + (j * 4 + gw) * ST::RPI;  // first row of instruction j
         tbk.id[j] = key < x.skv ? load_uniform(x.table_row + (key >> p.block_shift)) : 0;
       }
+    } else if constexpr (MEDIUM) {
+      const int key = key0 + 16 * gw;  // first of this wave's 16 rows
+      tbk.id[0] = key < x.skv ? load_uniform(x.table_row + (key >> p.block_shift)) : 0;
     } else {
       tbk.id[0] = (PAGED && key0 < x.skv) ? load_uniform(x.table_row + (key0 >> p.block_shift)) : 0;
     }
     return tbk;
   };
   auto issue_tile = [&](const Item& x, char* lds, const char* head, __amdgpu_buffer_rsrc_t rsrc, uint32_t rowb,
-                        uint32_t off, int64_t blk_stride, int tile, const TileBlocks& blk) {
+                        uint32_t off, int64_t blk_stride, int tile, const TileBlocks& blk, bool is_k) {
     const int key0 = tile * ST::kKeys;
-    if constexpr (SMALL) {
+    if constexpr (MEDIUM) {
+      // This wave's rows [key, key + 16) of the tile, one run in one page:
+      // instruction j loads rows key + j * RPI + 0..RPI-1 (scalar offset) into
+      // LDS rows 16 gw + j * RPI + ...  Both swizzles are linear in the row
+      // bits: V's depends on the lane's row lrow alone (off as given); K's
+      // chunk is (lane % CPR) ^ gk(lrow) ^ gk(j * RPI).
+      (void)rsrc;
+      (void)off;
+      typedef __attribute__((address_space(3))) void lds_void;
+      const int key = key0 + 16 * gw;
+      const int rows = x.skv - key;
+      __amdgpu_buffer_rsrc_t rt = make_rsrc(head, 0u);
+      if (rows > 0) {
+        const char* base = head + 2 * ((int64_t)blk.id[0] * blk_stride +
+                                       (int64_t)(key & ((1 << p.block_shift) - 1)) * (rowb >> 1));
+        rt = make_rsrc(base, (uint32_t)(min(rows, 16) - 1) * rowb + 2 * D);
+      }
+      const int lr = lane / CPR, lc = lane % CPR;
+#pragma unroll
+      for (int j = 0; j < ST::NI; ++j) {
+        const int sw = is_k ? (ST::gk(lr) ^ ST::gk(j * ST::RPI)) : ST::sv(lr);
+        const uint32_t o = (uint32_t)(lr * rowb) + 16u * (uint32_t)(lc ^ sw);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(lds + (gw * ST::NI + j) * 1024), 16, o,
+                                                 (uint32_t)(j * ST::RPI) * rowb, 0, 0);
+      }
+    } else if constexpr (SMALL) {
       // Instruction j loads rows [key, key + RPI) of the tile, one run in
       // one page (key is a multiple of RPI and pages hold >= RPI keys); its
       // descriptor ends at the sequence's last key.
@@ -388,10 +419,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
     }
   };
   auto issue_k = [&](const Item& x, char* lds, int tile, const TileBlocks& blk) {
-    issue_tile(x, lds, x.kbh, x.rk, kssb, koff, p.k.sb, tile, blk);
+    issue_tile(x, lds, x.kbh, x.rk, kssb, koff, p.k.sb, tile, blk, true);
   };
   auto issue_v = [&](const Item& x, char* lds, int tile, const TileBlocks& blk) {
-    issue_tile(x, lds, x.vbh, x.rv, vssb, voff, p.v.sb, tile, blk);
+    issue_tile(x, lds, x.vbh, x.rv, vssb, voff, p.v.sb, tile, blk, false);
   };
 
   // LDS side: per-lane read offsets (the 32-key block, chunk and row offsets
@@ -909,10 +940,12 @@ static hipError_t launch_paged_fwd_t(const FwdParams& p, int dtype, hipStream_t 
 }
 
 // Requires block_size >= 512 / D, the rows of one LDS-DMA instruction
-// (pages of >= 64 keys hold whole tiles; smaller ones whole instructions).
+// (pages of >= 64 keys hold whole tiles, of 16-32 keys whole 16-row wave
+// shares of a tile, smaller ones whole instructions).
 hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
   if ((1 << p.block_shift) < 512 / p.dm.D) return hipErrorInvalidValue;
-  return p.block_shift >= 6 ? launch_paged_fwd_t<1>(p, dtype, stream) : launch_paged_fwd_t<2>(p, dtype, stream);
+  if (p.block_shift >= 6) return launch_paged_fwd_t<1>(p, dtype, stream);
+  return p.block_shift >= 4 ? launch_paged_fwd_t<3>(p, dtype, stream) : launch_paged_fwd_t<2>(p, dtype, stream);
 }
 
 }  // namespace gqa
