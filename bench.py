@@ -122,10 +122,14 @@ def _time(torch, fn, steps, warmup, warm_ms=0.0):
         fn(0)
     torch.cuda.synchronize()
     if warm_ms > 0:
+        # (rotating the call index as the timed calls do, so that a config
+        # that rotates K/V sets meets the Infinity Cache in its steady state)
         t_end = time.perf_counter() + warm_ms * 1e-3
+        j = 0
         while time.perf_counter() < t_end:
             for _ in range(8):
-                fn(0)
+                fn(j)
+                j += 1
             torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
