@@ -38,12 +38,13 @@ SPLIT_MAX_ROWS = 64
 # least SPLIT_TILE keys), then doubles toward SPLIT_WG_PER_CU workgroups per
 # CU only while chunks keep at least this many keys: a workgroup's first
 # tiles and Q take 2-3 us to land, which short chunks do not amortise.
-# Measured on MI355X (bf16, rotating K/V sets), one token at G = 4: 16384
-# keys 32 splits 16.9 us / 64 splits 18.0, 32768 keys 27.6 / 29.5, 8192 keys
-# 12.3 / 12.5, 65536 and 131072 keys equal or better at 64; 16 tokens at
-# 32768 keys 35.7 / 41.5; 32 tokens at 32768 keys (128-row workgroups)
-# 256 workgroups 41 us, 512 51 us.
-SPLIT_WIDER_MIN_CHUNK = 1024
+# Measured on MI355X (bf16, rotating K/V sets), one token at G = 4 (the
+# 16-row first pass): 8192 keys 32 splits 11.5 us / 64 splits 11.8, 16384
+# keys 16.0 / 16.7, 32768 keys 25.6 / 27.3, 65536 keys 44.0-44.3 / 45.1-45.3,
+# 131072 keys 83.5-84.8 / 82.4-82.8 (so 64 only there); 16 tokens at 32768
+# keys 35.7 / 41.5; 32 tokens at 32768 keys (128-row workgroups) 256
+# workgroups 41 us, 512 51 us.
+SPLIT_WIDER_MIN_CHUNK = 2048
 # Shortest key cache worth splitting (the reference's threshold, dispatch.py:37).
 SPLIT_MIN_KV = 1024
 # Keys per split-KV tile; a chunk is never shorter than this many tiles

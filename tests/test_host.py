@@ -233,15 +233,14 @@ def test_route_baseline_configs():
     # decode 131072: split to 2 workgroups per CU
     r = choose_route(1, 32, 8, 1, 131072, cu)
     assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
-    # decode 8192 / 32768: one workgroup per CU (a second one only for chunks
-    # of at least 1024 keys)
+    # decode 8192 / 32768 / 65536: one workgroup per CU (a second one only
+    # for chunks of at least 2048 keys)
     r = choose_route(1, 32, 8, 1, 8192, cu)
     assert r.kind == "split" and r.splits == 32 and r.workgroups == 256
     r = choose_route(1, 32, 8, 1, 32768, cu)
     assert r.kind == "split" and r.splits == 32 and r.workgroups == 256
-    # ... 65536: two per CU with 1024-key chunks
     r = choose_route(1, 32, 8, 1, 65536, cu)
-    assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
+    assert r.kind == "split" and r.splits == 32 and r.workgroups == 256
     # head_dim 64 (the other first pass): two per CU with 128-key chunks
     r = choose_route(1, 32, 8, 1, 8192, cu, True, 64)
     assert r.kind == "split" and r.splits == 64
@@ -269,13 +268,13 @@ def test_route_wide_row_blocks():
     for sq in (9, 16):
         r = choose_route(1, 32, 8, sq, 131072, cu)
         assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
-        # 32768 keys: the CUs filled once (chunks of 1024 keys)
+        # 32768 keys: the CUs filled once
         assert choose_route(1, 32, 8, sq, 32768, cu).splits == 32
         r64 = choose_route(1, 32, 8, sq, 131072, cu, True, 64)
         assert r64.kind == "split" and r64.splits == 32 and r64.workgroups == 512
     assert choose_route(1, 32, 8, 8, 131072, cu).workgroups == 512
     # 65-128 rows: four 32-row blocks per workgroup; the split count fills
-    # the CUs, then doubles only while chunks keep 1024 keys
+    # the CUs, then doubles only while chunks keep 2048 keys
     r = choose_route(1, 32, 8, 17, 131072, cu)
     assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
     assert choose_route(1, 32, 8, 32, 32768, cu).splits == 32
@@ -368,8 +367,10 @@ def test_route_properties():
                 # never more splits than needed for the per-CU target
                 from gqa_kernels.dispatch import SPLIT_WG_PER_CU, SPLIT_WIDER_MIN_CHUNK
                 assert r.splits == 1 or (r.workgroups // 2) < SPLIT_WG_PER_CU * cu
-                # past one workgroup per CU only with chunks of >= 1024 keys
-                assert r.workgroups // 2 < cu or -(-skv // r.splits) >= SPLIT_WIDER_MIN_CHUNK
+                # a doubling past one workgroup per CU only with chunks of
+                # >= SPLIT_WIDER_MIN_CHUNK keys (no doubling at one split)
+                assert (r.splits == 1 or r.workgroups // 2 < cu
+                        or -(-skv // r.splits) >= SPLIT_WIDER_MIN_CHUNK)
 
 
 # ---------------------------------------------------------------------------
