@@ -54,14 +54,28 @@ __all__ = [
 LOG2E = math.log2(math.e)
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 
-# Split sizing, as for the contiguous decode route: one round of workgroups
-# at two per compute unit, chunks of at least two 128-key tiles.
+# Split sizing: a power of two split count that brings the first pass to a
+# number of workgroups per compute unit, every chunk keeping at least two
+# 128-key tiles.  Workgroups per CU: two for the register-staged first pass
+# (head_dim 64, pages of 1-2 keys); for the LDS-DMA first pass (head_dim
+# 128, pages of >= 4 keys) one, or four for a single-token step of a batch
+# of sequences over pages whose heads of a key are interleaved (token-major,
+# slot stride != head_dim).  Measured on MI355X (bf16, Hq = 32, Hkv = 8,
+# random block order, us): head-major 64-key pages, one token, 131072 keys
+# 32 / 64 splits 83.3 / 85.0, B = 4 x 32768 8 / 16 splits 81.0 / 84.6,
+# B = 16 x 8192 2 / 4 80.8 / 83.0, 16 tokens at 32768 keys 32 / 64 32.7 /
+# 39.2; token-major 16-key pages, one token, 131072 keys 32 / 64 87.8 /
+# 89.1, B = 4 x 32768 8 / 16 / 32 splits 90.3 / 88.3 / 86.4, B = 16 x 8192
+# 2 / 4 / 8 90.3 / 92.2 / 88.9; several tokens, B = 2 x 32768 16 tokens
+# 16 / 32 / 64 splits 56.6 / 58.4 / 71.3, B = 8 x 8192 4 tokens 4 / 8 / 16
+# 49.8 / 50.6 / 51.1.
 _SPLIT_ROWS = 32
 _SPLIT_WG_PER_CU = 2
+_LDS_WG_PER_CU = 1
+_LDS_WG_PER_CU_INTERLEAVED = 4
 _MIN_CHUNK = 256
 _SPLIT_MAX_ROWS = 64  # packed rows per kv head up to which the split-KV pass is used
 _SPLIT_MAX_ROWS_WIDE = 128  # ... at head_dim 128 with pages of >= 4 keys (128-row workgroups)
-_WIDE_MIN_CHUNK = 1024
 
 _cu_lock = threading.Lock()
 _cu_counts: dict = {}
@@ -86,35 +100,35 @@ def paged_chunk(max_seq_len: int, splits: int) -> int:
 
 
 def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
-                 cu_count: int, block_size: int = 64, head_dim: int = 128) -> int:
+                 cu_count: int, block_size: int = 64, head_dim: int = 128,
+                 heads_interleaved: bool = False) -> int:
     """Split count for a paged call: the power of two that brings the first
-    pass to two workgroups per compute unit while every chunk keeps at least
-    256 keys (pure function of the shapes).  With pages under 64 keys a chunk
-    spans at most GQA_PAGED_CHUNK_PAGES pages (the slice of the block table a
+    pass to its target workgroups per compute unit (at head_dim 128 with
+    pages of >= 4 keys one, or four for a single-token step of a batch over
+    pages whose heads are interleaved; else two) while every chunk keeps at
+    least 256 keys (pure function of the shapes and of ``heads_interleaved``:
+    the cache's slot stride differs from head_dim).  With pages under 64 keys a chunk spans
+    at most GQA_PAGED_CHUNK_PAGES pages (the slice of the block table a
     workgroup stages in LDS), which can ask for more splits."""
     group = num_heads // num_kv_heads
     rows = group * seq_q
     # Rows per first-pass workgroup: up to four 32-row blocks at head_dim 128
     # with pages of >= 4 keys (the LDS-DMA first pass), else one.
+    lds_pass = head_dim == 128 and block_size >= 4
     rpw = _SPLIT_ROWS
-    if head_dim == 128 and block_size >= 4 and rows > _SPLIT_ROWS:
+    if lds_pass and rows > _SPLIT_ROWS:
         rpw = 2 * _SPLIT_ROWS if rows <= 2 * _SPLIT_ROWS else 4 * _SPLIT_ROWS
     base = -(-rows // rpw) * num_kv_heads * batch
-    target = _SPLIT_WG_PER_CU * cu_count
-    splits = 1
-    if rpw > 2 * _SPLIT_ROWS:
-        # 128-row workgroups: fill the compute units, then more splits only
-        # while chunks keep _WIDE_MIN_CHUNK keys (as the contiguous route).
-        while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
-               and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
-            splits *= 2
-        while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
-               and -(-max_seq_len // (splits * 2)) >= _WIDE_MIN_CHUNK):
-            splits *= 2
+    if lds_pass:
+        wide = heads_interleaved and batch > 1 and seq_q == 1
+        per_cu = _LDS_WG_PER_CU_INTERLEAVED if wide else _LDS_WG_PER_CU
     else:
-        while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
-               and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
-            splits *= 2
+        per_cu = _SPLIT_WG_PER_CU
+    target = per_cu * cu_count
+    splits = 1
+    while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
+           and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
+        splits *= 2
     if block_size < 64:
         def too_many_pages(s):
             return paged_chunk(max_seq_len, s) // block_size > _lib.GQA_PAGED_CHUNK_PAGES
@@ -244,8 +258,9 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     assert 0 <= max_seq_len <= capacity, "max_seq_len exceeds the block table's capacity"
     dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
     if splits is None:
+        interleaved = k_cache.stride(1) != head_dim or v_cache.stride(1) != head_dim
         splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), block_size,
-                              head_dim)
+                              head_dim, interleaved)
     if scale is None:
         scale = head_dim ** -0.5
 

@@ -283,8 +283,8 @@ def test_route_wide_row_blocks():
     assert choose_route(1, 32, 8, 33, 131072, cu).kind == "chunks"  # past the split path: key chunks
     assert choose_route(1, 32, 8, 17, 131072, cu, True, 64).kind == "chunks"  # head_dim 64: 64 rows at most
     assert paged_splits(1, 32, 8, 32, 32768, cu) == 32
-    assert paged_splits(1, 32, 8, 16, 131072, cu) == 64
-    assert paged_splits(1, 32, 8, 16, 131072, cu, block_size=16) == 64
+    assert paged_splits(1, 32, 8, 16, 131072, cu) == 32
+    assert paged_splits(1, 32, 8, 16, 131072, cu, block_size=16) == 32
     assert paged_splits(1, 32, 8, 16, 131072, cu, head_dim=64) == 32
 
 

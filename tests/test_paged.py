@@ -218,8 +218,18 @@ def test_strerror_block(lib):
 # ---------------------------------------------------------------------------
 def test_paged_splits():
     from gqa_kernels.paged import paged_splits
-    # one 32-row block per kv head: 8 workgroups per split, 512 targeted
-    assert paged_splits(1, 32, 8, 1, 131072, 256) == 64
+    # one 32-row block per kv head: 8 workgroups per split; the LDS-DMA first
+    # pass (head_dim 128, pages of >= 4 keys) fills the 256 CUs once
+    assert paged_splits(1, 32, 8, 1, 131072, 256) == 32
+    assert paged_splits(1, 32, 8, 1, 131072, 256, heads_interleaved=True) == 32
+    # a single-token step of a batch over token-major pages (heads
+    # interleaved): four per CU; several tokens: one
+    assert paged_splits(4, 32, 8, 1, 32768, 256) == 8
+    assert paged_splits(4, 32, 8, 1, 32768, 256, heads_interleaved=True) == 32
+    assert paged_splits(4, 32, 8, 4, 32768, 256, heads_interleaved=True) == 8
+    # head_dim 64 / pages of 1-2 keys (register-staged first pass): two per CU
+    assert paged_splits(1, 32, 8, 1, 131072, 256, head_dim=64) == 64
+    assert paged_splits(1, 32, 8, 1, 131072, 256, block_size=2) == 64
     assert paged_splits(64, 32, 8, 1, 4096, 256) == 1
     assert paged_splits(1, 32, 8, 1, 300, 256) == 1
     for L in (256, 1000, 5000, 1 << 20):
