@@ -367,7 +367,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
       // bits: V's depends on the lane's row lrow alone (off as given); K's
       // chunk is (lane % CPR) ^ gk(lrow) ^ gk(j * RPI).
       (void)rsrc;
-      (void)off;
       typedef __attribute__((address_space(3))) void lds_void;
       const int key = key0 + 16 * gw;
       const int rows = x.skv - key;
@@ -377,13 +376,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
                                        (int64_t)(key & ((1 << p.block_shift) - 1)) * (rowb >> 1));
         rt = make_rsrc(base, (uint32_t)(min(rows, 16) - 1) * rowb + 2 * D);
       }
-      const int lr = lane / CPR, lc = lane % CPR;
+      if constexpr (D == 64) {
+        // Derived from `off` (the lane's offset for LDS rows gw * RPI + lr),
+        // so no offsets of their own stay live across the loop: sv depends
+        // on lr alone, so V's is `off` for both instructions; gk(gw * RPI +
+        // lr) = gk(lr) ^ gk(8 (gw & 1)) with gk(8) = 2, so K's is `off` for
+        // instruction j = gw & 1 and `off` with chunk bit 1 flipped (byte
+        // offset ^ 32, as lr * rowb is a multiple of 64: the host takes
+        // this path only for such row strides) for the other.
+        // The empty asm keeps the XOR here: hoisted out of the tile loop, its
+        // result would hold a register across the loop.
+        (void)lane;
+        uint32_t flip = off;
+        if (is_k) {
+          asm volatile("" : "+v"(flip));
+          flip ^= 32u;
+        }
+        const uint32_t other = flip;
 #pragma unroll
-      for (int j = 0; j < ST::NI; ++j) {
-        const int sw = is_k ? (ST::gk(lr) ^ ST::gk(j * ST::RPI)) : ST::sv(lr);
-        const uint32_t o = (uint32_t)(lr * rowb) + 16u * (uint32_t)(lc ^ sw);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(lds + (gw * ST::NI + j) * 1024), 16, o,
-                                                 (uint32_t)(j * ST::RPI) * rowb, 0, 0);
+        for (int j = 0; j < ST::NI; ++j) {
+          const uint32_t o = (j == (gw & 1)) ? off : other;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(lds + (gw * ST::NI + j) * 1024), 16, o,
+                                                   (uint32_t)(j * ST::RPI) * rowb, 0, 0);
+        }
+      } else {
+        (void)off;
+        const int lr = lane / CPR, lc = lane % CPR;
+#pragma unroll
+        for (int j = 0; j < ST::NI; ++j) {
+          const int sw = is_k ? (ST::gk(lr) ^ ST::gk(j * ST::RPI)) : ST::sv(lr);
+          const uint32_t o = (uint32_t)(lr * rowb) + 16u * (uint32_t)(lc ^ sw);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(lds + (gw * ST::NI + j) * 1024), 16, o,
+                                                   (uint32_t)(j * ST::RPI) * rowb, 0, 0);
+        }
       }
     } else if constexpr (SMALL) {
       // Instruction j loads rows [key, key + RPI) of the tile, one run in
@@ -941,11 +966,15 @@ static hipError_t launch_paged_fwd_t(const FwdParams& p, int dtype, hipStream_t 
 
 // Requires block_size >= 512 / D, the rows of one LDS-DMA instruction
 // (pages of >= 64 keys hold whole tiles, of 16-32 keys whole 16-row wave
-// shares of a tile, smaller ones whole instructions).
+// shares of a tile, smaller ones whole instructions).  The 16-32-key form at
+// D = 64 derives its K offsets by an XOR of bit 5 and so takes row strides
+// of a multiple of 64 bytes; other strides take the per-instruction form,
+// which serves any page of >= 8 keys there.
 hipError_t launch_paged_fwd(const FwdParams& p, int dtype, hipStream_t stream) {
   if ((1 << p.block_shift) < 512 / p.dm.D) return hipErrorInvalidValue;
   if (p.block_shift >= 6) return launch_paged_fwd_t<1>(p, dtype, stream);
-  return p.block_shift >= 4 ? launch_paged_fwd_t<3>(p, dtype, stream) : launch_paged_fwd_t<2>(p, dtype, stream);
+  const bool medium = p.block_shift >= 4 && (p.dm.D != 64 || (2 * p.k.ss) % 64 == 0);
+  return medium ? launch_paged_fwd_t<3>(p, dtype, stream) : launch_paged_fwd_t<2>(p, dtype, stream);
 }
 
 }  // namespace gqa

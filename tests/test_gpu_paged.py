@@ -109,6 +109,8 @@ def test_paged_attention_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, caus
     (2, 32, 8, 90, [999, 400], 128, 32, torch.float16, False, True),         # 32-key blocks, fp16
     (2, 16, 4, 70, [701, 333], 64, 8, torch.float16, True, False),           # smallest block at D = 64
     (1, 16, 2, 120, [1500], 64, 16, torch.bfloat16, False, True),            # D = 64, 16-key HND
+    (2, 16, 2, 120, [1500, 433], 64, 16, torch.bfloat16, True, False),       # D = 64, 16-key NHD
+    (2, 16, 4, 80, [900, 2000], 64, 32, torch.float16, True, False),         # D = 64, 32-key NHD
     (2, 32, 8, 100, [0, 700], 128, 64, torch.bfloat16, True, False),         # a sequence without keys: zeros
 ])
 def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, causal, hnd):
@@ -129,7 +131,31 @@ def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, ca
     _check(o_split, None, q, kc, vc, table, seq_lens, causal, dtype)
 
 
-@pytest.mark.parametrize("D,bs", [(128, 128), (128, 16), (128, 4), (64, 8)])
+@pytest.mark.parametrize("pad", [32, 16])
+def test_paged_single_pass_padded_rows(pad):
+    """Caches whose slot stride is head_dim + pad elements (one kv head):
+    at D = 64 a row stride of 192 bytes (a multiple of 64, not of 128) keeps
+    the 16-32-key form, whose K offsets come from an XOR of bit 5; 160 bytes
+    takes the per-instruction form."""
+    from gqa_kernels.paged import paged_attention, paged_route
+    B, Hq, Hkv, Sq, lens, D, bs = 2, 8, 1, 100, [777, 1500], 64, 16
+    assert paged_route(Hq, Hkv, Sq, bs, D) == "single"
+    q, kc, vc, table, seq_lens = _paged_inputs(B, Hq, Hkv, Sq, lens, D, bs, torch.bfloat16, seed=pad)
+    print(f"paged single padded rows D={D} bs={bs} pad={pad}", flush=True)
+
+    def padded(t):
+        store = torch.full(t.shape[:-1] + (D + pad,), float("nan"), dtype=t.dtype, device=DEV)
+        store[..., :D] = t.to(DEV)
+        return store[..., :D]
+    kd, vd = padded(kc), padded(vc)
+    assert kd.stride(1) == D + pad
+    o, lse = paged_attention(q.to(DEV), kd, vd, table.to(DEV), seq_lens.to(DEV), True, max_seq_len=max(lens),
+                             return_lse=True)
+    torch.cuda.synchronize()
+    _check(o, lse, q, kc, vc, table, seq_lens, True, torch.bfloat16)
+
+
+@pytest.mark.parametrize("D,bs", [(128, 128), (128, 16), (128, 4), (64, 8), (64, 16)])
 def test_paged_single_pass_equals_contiguous_prefill_chunk(D, bs):
     """The chunked-prefill BASELINE shape (B=4, 512 new tokens over 8192 keys)
     from a shuffled block cache vs the contiguous single pass: bit-identical
