@@ -85,20 +85,22 @@ def hbm_bytes(b, hq, hkv, sq, skv, d, elem=2) -> int:
     return elem * d * (2 * b * hkv * skv + 2 * b * hq * sq)
 
 
-def _inputs(torch, b, hq, hkv, sq, skv, d, n_kv_sets=1, scale=1.0):
-    """q and n_kv_sets (k, v) pairs, bf16 on the GPU.  q and the first k, v
-    are N(0,1) draws (times `scale`) from a CPU generator seeded 0, in the
-    order q, k, v, rounded to bf16 from fp32.  The further K/V sets, which
-    only keep consecutive calls of an HBM-bound config from finding their
-    keys in the Infinity Cache, and tensors above CPU_DRAW_MAX_ELEMS come
-    from a seeded GPU generator (also N(0,1) times `scale`)."""
+def _inputs(torch, b, hq, hkv, sq, skv, d, n_kv_sets=1, scale=1.0, dtype=None):
+    """q and n_kv_sets (k, v) pairs on the GPU, bf16 unless `dtype` says
+    otherwise.  q and the first k, v are N(0,1) draws (times `scale`) from a
+    CPU generator seeded 0, in the order q, k, v, rounded from fp32.  The
+    further K/V sets, which only keep consecutive calls of an HBM-bound
+    config from finding their keys in the Infinity Cache, and tensors above
+    CPU_DRAW_MAX_ELEMS come from a seeded GPU generator (also N(0,1) times
+    `scale`)."""
+    dt = torch.bfloat16 if dtype is None else dtype
     g = torch.Generator(device="cpu").manual_seed(0)
     gg = torch.Generator(device="cuda").manual_seed(1)
 
     def draw(shape, cpu):
         if cpu and math.prod(shape) <= CPU_DRAW_MAX_ELEMS:
-            return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16).to("cuda")
-        return (torch.randn(shape, device="cuda", generator=gg) * scale).to(torch.bfloat16)
+            return (torch.randn(shape, generator=g) * scale).to(dt).to("cuda")
+        return (torch.randn(shape, device="cuda", generator=gg) * scale).to(dt)
 
     q = draw((b, hq, sq, d), True)
     kvs = [(draw((b, hkv, skv, d), i == 0), draw((b, hkv, skv, d), i == 0)) for i in range(n_kv_sets)]
@@ -516,10 +518,18 @@ CONFIGS = (
 # Shapes beyond the BASELINE configs that exercise the other routes (timed
 # in the default run as ``extras``): a verify step of 16 tokens (64 packed
 # rows per kv head: the decode first pass with 64-row workgroups) and a
-# 128-token chunk (the single pass over key chunks), both against 131072 keys.
+# 128-token chunk (the single pass over key chunks), both against 131072 keys;
+# then the headline prefill and decode in fp16 (the other input type the
+# reference accepts, dispatch.py:18) and with the LSE side output
+# (return_lse=True).  Optional trailing fields: dtype ("bf16" default,
+# "fp16") and return_lse.
 EXTRAS = (
     ("verify 16 x 131072", 1, 32, 8, 16, 131072, "hbm", 128),
     ("chunk 128 x 131072", 1, 32, 8, 128, 131072, "mfma", 128),
+    ("prefill 16384 fp16", 1, 32, 8, 16384, 16384, "mfma", 128, "fp16"),
+    ("decode 131072 fp16", 1, 32, 8, 1, 131072, "hbm", 128, "fp16"),
+    ("prefill 16384 return_lse", 1, 32, 8, 16384, 16384, "mfma", 128, "bf16", True),
+    ("decode 131072 return_lse", 1, 32, 8, 1, 131072, "hbm", 128, "bf16", True),
 )
 # Untimed calls of every config beyond the headline run for at least this
 # long before its timed calls (its inputs were just drawn on the host, the
@@ -548,19 +558,26 @@ def sweep(torch, gqa_flash_attn, steps=20, warmup=5, only=None, table=CONFIGS):
     sel = table
     if only is not None:  # the config of that exact name, else those starting with it
         sel = [c for c in table if c[0] == only] or [c for c in table if c[0].startswith(only)]
-    for name, b, hq, hkv, sq, skv, bound, d in sel:
+    for name, b, hq, hkv, sq, skv, bound, d, *opt in sel:
+        dtype_s = opt[0] if opt else "bf16"
+        lse = bool(opt[1]) if len(opt) > 1 else False
         by1 = hbm_bytes(b, hq, hkv, sq, skv, d)
         nset = max(1, math.ceil(ROTATE_BYTES / by1)) if bound == "hbm" else 1
-        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, d, n_kv_sets=nset)
+        q, kvs = _inputs(torch, b, hq, hkv, sq, skv, d, n_kv_sets=nset,
+                         dtype=torch.float16 if dtype_s == "fp16" else torch.bfloat16)
         n = steps * 5 if bound == "hbm" else steps
-        ms = _time(torch, lambda i: gqa_flash_attn(q, *kvs[i % nset], causal=True), n, warmup, warm_ms=WARM_MS)
+        if lse:
+            call = lambda i: gqa_flash_attn(q, *kvs[i % nset], causal=True, return_lse=True)  # noqa: E731
+        else:
+            call = lambda i: gqa_flash_attn(q, *kvs[i % nset], causal=True)  # noqa: E731
+        ms = _time(torch, call, n, warmup, warm_ms=WARM_MS)
         fl = flops(b, hq, sq, skv, d)
         tflops, gbs = fl / (ms * 1e-3) / 1e12, by1 / (ms * 1e-3) / 1e9
         achieved, peak, unit = (tflops, PEAK_BF16_TFLOPS, "TFLOP/s") if bound == "mfma" else \
             (gbs, PEAK_HBM_GBS, "GB/s")
         route = choose_route(b, hq, hkv, sq, skv, _cu_count(0), causal=True, head_dim=d)
         rows.append({"config": name, "B": b, "Hq": hq, "Hkv": hkv, "seq_q": sq, "seq_kv": skv, "D": d,
-                     "us": ms * 1e3, "tflops": tflops, "gbs": gbs, "steps": n, "kv_sets": nset,
+                     "dtype": dtype_s, "return_lse": lse, "us": ms * 1e3, "tflops": tflops, "gbs": gbs, "steps": n, "kv_sets": nset,
                      "route": route.kind + (f" splits={route.splits}" if route.kind in ("split", "chunks") else
                                             f" key-split blocks={route.fwd_split}" if route.fwd_split else ""),
                      "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
