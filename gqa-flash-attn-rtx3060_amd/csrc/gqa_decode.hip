@@ -225,7 +225,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int D = kDecD;
   constexpr bool PAGED = KV != 0;
   using E = Elem<DT>;
-  using T = typename E::T;
   using ST = FwdStage<D>;
   constexpr int CPR = ST::CPR;
   constexpr int NKS = D / 16;  // k-steps of S^T

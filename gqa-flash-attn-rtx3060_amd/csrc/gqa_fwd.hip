@@ -61,8 +61,7 @@ namespace gqa {
 // still -inf after the exact pass (every key masked so far) uses 0 as the
 // reference, so a fully masked tile contributes p = 0, never NaN.
 // ---------------------------------------------------------------------------
-constexpr float kRescaleLog2 = 8.0f;
-constexpr float kRescaleSum = 256.0f;  // 2^kRescaleLog2
+constexpr float kRescaleSum = 256.0f;  // 2^8
 
 // Exact pass: the tile's row max (a max3 tree), m_ref raised to it, l and the
 // accumulators rescaled.  Returns -m_ref * c, the offset of the exponent.
@@ -536,9 +535,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   TileBlocks blk_next = prologue_kv(it);
   prologue_q(it);
 
-  // MFMA phase tt: P*V of tile tt-1 and S^T of tile tt, from stage tt (ring
-  // slot tt % 3).
-  auto mphase = [&](auto s3, auto pvc, auto sc_, int tt) {
+  // MFMA phase of tile tt: P*V of tile tt-1 and S^T of tile tt, from ring
+  // slot s3 = tt % 3.
+  auto mphase = [&](auto s3, auto pvc, auto sc_) {
     constexpr bool DO_PV = decltype(pvc)::value;
     constexpr bool DO_S = decltype(sc_)::value;
     constexpr int NPV = DO_PV ? 4 * NDB : 0;
@@ -670,31 +669,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
 
     const int ntiles = it.ntiles;
     if (ntiles > 0) {
-      mphase(I0{}, BF{}, BT{}, 0);
+      mphase(I0{}, BF{}, BT{});
       vphase(I0{}, 0);
       int tt = 1;
       for (; tt + 3 <= ntiles; tt += 3) {
-        mphase(I1{}, BT{}, BT{}, tt);
+        mphase(I1{}, BT{}, BT{});
         vphase(I1{}, tt);
-        mphase(I2{}, BT{}, BT{}, tt + 1);
+        mphase(I2{}, BT{}, BT{});
         vphase(I2{}, tt + 1);
-        mphase(I0{}, BT{}, BT{}, tt + 2);
+        mphase(I0{}, BT{}, BT{});
         vphase(I0{}, tt + 2);
       }
       if (tt < ntiles) {
-        mphase(I1{}, BT{}, BT{}, tt);
+        mphase(I1{}, BT{}, BT{});
         vphase(I1{}, tt);
         ++tt;
         if (tt < ntiles) {
-          mphase(I2{}, BT{}, BT{}, tt);
+          mphase(I2{}, BT{}, BT{});
           vphase(I2{}, tt);
           ++tt;
         }
       }
       const int s3 = tt % 3;
-      if (s3 == 0) mphase(I0{}, BT{}, BF{}, tt);
-      else if (s3 == 1) mphase(I1{}, BT{}, BF{}, tt);
-      else mphase(I2{}, BT{}, BF{}, tt);
+      if (s3 == 0) mphase(I0{}, BT{}, BF{});
+      else if (s3 == 1) mphase(I1{}, BT{}, BF{});
+      else mphase(I2{}, BT{}, BF{});
     } else {
       phase_barrier();
     }
