@@ -643,23 +643,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // by sv16(r) = 2 (r & 7): the 8 rows one half-wave's transposing read
 // touches (two lane groups x 4 keys) then cover all 64 banks once.  Wave w
 // accumulates O^T for dims [32 w, 32 w + 32) as two 16-dim blocks.
+// Head_dim 64 (128-byte rows, 8 rows per LDS-DMA instruction): wave w takes
+// dims [16 w, 16 w + 16), one block, and V is swizzled by sv16(r) = r & 6
+// (a half-wave's 8 rows x 32 bytes: rows of one parity share a bank half,
+// and r & 6 gives their four 32-byte pieces four distinct bank groups); the
+// fused combine is not built for it (its callers take the two-launch form).
 // ---------------------------------------------------------------------------
-template <int DT, int KV>
+template <int DT, int KV, int D = kDecD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gqa_decode16_kernel(SplitParams p) {
-  constexpr int D = kDecD;
+  static_assert(D == 128 || D == 64, "head_dim 64 or 128");
   constexpr bool PAGED = KV != 0;
   using E = Elem<DT>;
   using ST = FwdStage<D>;
   constexpr int CPR = ST::CPR;
   constexpr int NI = ST::NI;    // LDS-DMA instructions per wave per K (or V) tile
   constexpr int NKS = D / 32;   // k-steps of S^T
-  // LDS as gqa_decode_kernel: two stages (64 KiB, two workgroups per CU;
-  // a third stage for grids of one workgroup per CU measured slower at 8K-32K
-  // keys), reused by the fused combine.
-  __shared__ __attribute__((aligned(1024))) char lds_a_k0[kDecTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_b_v0[kDecTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_c_k1[kDecTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_d_v1[kDecTileBytes];
+  constexpr int NDB = D / 64;   // 16-dim blocks of O^T per wave
+  // The V swizzle (chunk XOR) of tile row r: a function of r & 7.
+  auto sv16 = [](int r) { return D == 128 ? 2 * (r & 7) : (r & 6); };
+  // LDS as gqa_decode_kernel: two stages (64 KiB at head_dim 128, two
+  // workgroups per CU; a third stage for grids of one workgroup per CU
+  // measured slower at 8K-32K keys), reused by the fused combine.
+  __shared__ __attribute__((aligned(1024))) char lds_a_k0[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b_v0[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_c_k1[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_d_v1[ST::kTileBytes];
   __shared__ int s_last;
 
   const Dims& dm = p.dm;
@@ -711,14 +719,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     return it >= ntiles ? it : (j >= ntiles ? j - ntiles : j);
   };
 
-  // LDS-DMA source offsets of this lane: its row within an instruction's 4
-  // rows, its chunk swizzled by gk (K) or sv16 (V) of the tile row, whose
-  // low three bits are 4 (wave & 1) + lrow for every instruction this wave
-  // issues (instruction j of wave w loads rows 16 j + 4 w + 0..3).
+  // LDS-DMA source offsets of this lane: its row within an instruction's
+  // RPI rows, its chunk swizzled by gk (K) or sv16 (V) of the tile row, whose
+  // low bits are those of RPI w + lrow for every instruction this wave issues
+  // (instruction j of wave w loads rows RPI (4 j + w) + 0..RPI-1).
   const int lrow = lane / CPR;
   const uint32_t koff =
       (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ ST::gk((wave * ST::RPI + lrow) & 15));
-  const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ (2 * ((4 * (wave & 1) + lrow) & 7)));
+  const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ sv16(wave * ST::RPI + lrow));
   auto issue = [&](int it, char* kst, char* vst) {
     const int j = tile_rel(it) * 64;
     if constexpr (KV == 0) {
@@ -738,8 +746,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       issue_tile_dma<D, kDmaStream>(vst, tv, 0u, vssb, voff, wave);
     } else if constexpr (KV == 3) {
       // Pages of 16-32 keys: this wave loads rows [key, key + 16) of the
-      // tile (one page; as gqa_decode_kernel).  The V swizzle sv16 of row
-      // 16 wave + 4 jj + lrow is 2 (4 (jj & 1) + lrow).
+      // tile (one page; as gqa_decode_kernel).  Instruction jj loads rows
+      // 16 wave + RPI jj + lrow, whose V swizzle is sv16(RPI jj + lrow).
       typedef __attribute__((address_space(3))) void lds_void;
       const int key = c0 + j + 16 * wave, rows = c1 - key;
       __amdgpu_buffer_rsrc_t tk = make_rsrc(kbase, 0u), tv = make_rsrc(vbase, 0u);
@@ -754,7 +762,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int jj = 0; jj < NI; ++jj) {
         const uint32_t ko = (uint32_t)(lrow * kssb) +
                             16u * (uint32_t)((lane % CPR) ^ ST::gk(lrow) ^ ST::gk(jj * ST::RPI));
-        const uint32_t vo = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ (2 * (4 * (jj & 1) + lrow)));
+        const uint32_t vo = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ sv16(jj * ST::RPI + lrow));
         __builtin_amdgcn_raw_ptr_buffer_load_lds(tk, (lds_void*)(kst + (wave * NI + jj) * 1024), 16, ko,
                                                  (uint32_t)(jj * ST::RPI) * kssb, 0, kDmaStream);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(tv, (lds_void*)(vst + (wave * NI + jj) * 1024), 16, vo,
@@ -802,21 +810,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // LDS read offsets.  K: row 16 kb + i16, chunk 4 ks + lg (16 lanes of a
   // lane group read 16 rows at distinct swizzled chunks: conflict-free).
   // V: the first run's row 4 lg + jj / 4 (jj = lane within its 16-lane
-  // group), dims 32 wave + 16 db + 4 (jj % 4).
+  // group), dims (D / 4) wave + 16 db + 4 (jj % 4).
   uint32_t ka[NKS];
 #pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) ka[ks] = (uint32_t)(i16 * (2 * D) + 16 * ((4 * ks + lg) ^ ST::gk(i16))) & 0xFF0u;
-  uint32_t vb[2];
+  for (int ks = 0; ks < NKS; ++ks)
+    ka[ks] = (uint32_t)(i16 * (2 * D) + 16 * ((4 * ks + lg) ^ ST::gk(i16))) & (uint32_t)((32 * D - 1) & ~15);
+  uint32_t vb[NDB];
   {
     const int jj = lane & 15;
     const int rr = 4 * lg + (jj >> 2);
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
-      vb[db] = (uint32_t)(rr * (2 * D) + 16 * ((4 * wave + 2 * db + ((jj & 3) >> 1)) ^ (2 * (rr & 7))) + 8 * (jj & 1)) &
-               0xFF8u;
+    for (int db = 0; db < NDB; ++db)
+      vb[db] = (uint32_t)(rr * (2 * D) + 16 * (((D / 32) * wave + 2 * db + ((jj & 3) >> 1)) ^ sv16(rr)) + 8 * (jj & 1)) &
+               (uint32_t)((32 * D - 1) & ~7);
   }
 
-  f32x4 acc[2] = {};
+  f32x4 acc[NDB] = {};
   float m_run = -__builtin_inff(), l_run = 0.f;
   const float c = dm.c;
 
@@ -891,11 +900,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     l_run = l_run * alpha + rs;
     m_run = m_new;
 #pragma unroll
-    for (int db = 0; db < 2; ++db) acc[db] *= alpha;
+    for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
 
     // O^T (this wave's dims) += V^T P^T over the 64 keys.
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const u32x2 lo = ld_tr(cv + vb[db] + (32 * j) * (2 * D));
@@ -926,22 +935,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // This wave's dims of the valid rows' partials: lane (i16, lg) holds dims
-  // 32 wave + 16 db + 4 lg + 0..3 in acc[db]; l is summed over the 4 lane
+  // (D / 4) wave + 16 db + 4 lg + 0..3 in acc[db]; l is summed over the 4 lane
   // groups (each holds the sum over its own keys).
   const float l_tot = xhalf_sum(xquad_sum(l_run));
   if (valid) {
     const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
-      store_coherent4(rw, (uint32_t)((row * D + 32 * wave + 16 * db + 4 * lg) * 4), acc[db]);
+    for (int db = 0; db < NDB; ++db)
+      store_coherent4(rw, (uint32_t)((row * D + (D / 4) * wave + 16 * db + 4 * lg) * 4), acc[db]);
     if (wave == 0 && lg == 0) {
       store_coherent(p.ws_m + row, skv == 0 ? 0.f : m_run * c);
       store_coherent(p.ws_l + row, l_tot);
     }
   }
 
-  if (PAGED || p.counters == nullptr) return;
+  if (PAGED || D != kDecD || p.counters == nullptr) return;
   // Fused combine, as gqa_decode_kernel.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -958,18 +967,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 bool decode_kernel_fits(const SplitParams& p) {
-  if (p.dm.D != kDecD) return false;
+  const int D = p.dm.D;
+  // Head_dim 64: the 16-row first pass only (at most 16 packed rows per kv
+  // head), in the two-launch form (no fused combine at that width).
+  if (D == 64) {
+    if (p.dm.G * p.dm.Sq > 16 || p.counters != nullptr) return false;
+  } else if (D != kDecD) {
+    return false;
+  }
   const bool paged = p.block_table != nullptr;
-  // Paged: whole LDS-DMA instructions (4 rows at head_dim 128) in a page,
-  // and 64-key-aligned chunks (so a tile lies in a page of >= 64 keys).
-  if (paged && ((1 << p.block_shift) < FwdStage<kDecD>::RPI || (p.chunk & 63) != 0)) return false;
+  // Paged: whole LDS-DMA instructions (512 / D rows) in a page, and
+  // 64-key-aligned chunks (so a tile lies in a page of >= 64 keys).
+  if (paged && ((1 << p.block_shift) < 512 / D || (p.chunk & 63) != 0)) return false;
   // 32-bit descriptor offsets: (contiguous) a chunk plus a tile of K and V
   // rows, (paged) a tile of rows; the whole accumulator workspace.
   const int64_t span = paged ? 64 : (int64_t)p.chunk + 64;
   if (span * p.k.ss * 2 >= ((int64_t)1 << 31) || span * p.v.ss * 2 >= ((int64_t)1 << 31)) return false;
-  const int64_t acc_bytes = (int64_t)p.dm.B * p.dm.Hq * p.dm.Sq * p.splits * kDecD * 4;
+  const int64_t acc_bytes = (int64_t)p.dm.B * p.dm.Hq * p.dm.Sq * p.splits * D * 4;
   // ... and a kv head's query group (its G heads x Sq rows).
-  const int64_t q_bytes = 2 * ((int64_t)(p.dm.G - 1) * p.q.sh + (int64_t)(p.dm.Sq - 1) * p.q.ss + kDecD);
+  const int64_t q_bytes = 2 * ((int64_t)(p.dm.G - 1) * p.q.sh + (int64_t)(p.dm.Sq - 1) * p.q.ss + D);
   return acc_bytes <= 0xFFFFFFF0ll && q_bytes < ((int64_t)1 << 31);
 }
 
@@ -980,7 +996,9 @@ static hipError_t launch_decode_t(const SplitParams& p, hipStream_t stream) {
   const int rw = p.n_rblk >= 3 ? 4 : p.n_rblk == 2 ? 2 : 1;
   const int64_t total = (int64_t)p.dm.B * p.dm.Hkv * ((p.n_rblk + rw - 1) / rw) * p.splits;
   if (total <= 0) return hipSuccess;
-  if (p.dm.G * p.dm.Sq <= 16)
+  if (p.dm.D == 64)  // decode_kernel_fits: at most 16 packed rows
+    hipLaunchKernelGGL((gqa_decode16_kernel<DT, KV, 64>), dim3((unsigned)total), dim3(256), 0, stream, p);
+  else if (p.dm.G * p.dm.Sq <= 16)
     hipLaunchKernelGGL((gqa_decode16_kernel<DT, KV>), dim3((unsigned)total), dim3(256), 0, stream, p);
   else if (rw == 4)
     hipLaunchKernelGGL((gqa_decode_kernel<DT, KV, 4>), dim3((unsigned)total), dim3(256), 0, stream, p);

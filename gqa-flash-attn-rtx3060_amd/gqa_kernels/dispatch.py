@@ -55,6 +55,13 @@ SPLIT_MIN_TILES = 1
 # Target workgroups per compute unit for the split-KV first pass (the kernel
 # runs two per CU at once; one round of workgroups measured fastest).
 SPLIT_WG_PER_CU = 2
+# Packed rows per kv head up to which head_dim 64 also runs the 16-row
+# LDS-DMA first pass, and with it the head_dim-128 split count.  Measured on
+# MI355X (bf16, one token, G = 4, rotating K/V sets, us): 32768 keys 32
+# splits 17.3 / 64 18.2 (register-staged pass: 20.1 at 64), 131072 keys 32
+# 46.8 / 64 45.9 / 128 50.3 (47.9 at 64), B = 4 x 32768 8 46.7 / 16 46.0 /
+# 32 50.5, 8192 keys 32 10.9 / 64 10.7.
+DEC16_ROWS = 16
 # Single pass with key-range split of the heaviest causal query blocks: only
 # considered while there are fewer than this many workgroups per CU, and
 # taken when the modelled run time drops by at least FWD_SPLIT_GAIN.
@@ -229,14 +236,17 @@ def split_max_rows(head_dim: int = 128) -> int:
     return SPLIT_WIDER_ROWS if head_dim == 128 else SPLIT_MAX_ROWS
 
 
-def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int, head_dim: int = 128) -> int:
+def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int, head_dim: int = 128,
+                rows16: bool = False) -> int:
     """Split count of the split-KV path for `base` workgroups per split
-    (head_dim 128: fill the CUs, then a second workgroup per CU only for
-    chunks of SPLIT_WIDER_MIN_CHUNK keys; head_dim 64: two workgroups per CU
-    with chunks of SPLIT_MIN_TILES tiles)."""
+    (head_dim 128, and head_dim 64 when the 16-row first pass runs
+    (`rows16`: at most DEC16_ROWS packed rows): fill the CUs, then a second
+    workgroup per CU only for chunks of SPLIT_WIDER_MIN_CHUNK keys; head_dim
+    64 over more rows: two workgroups per CU with chunks of SPLIT_MIN_TILES
+    tiles)."""
     target = SPLIT_WG_PER_CU * cu_count
     splits = 1
-    if head_dim == 128 or rows_per_wg > SPLIT_WIDE_ROWS:
+    if head_dim == 128 or rows_per_wg > SPLIT_WIDE_ROWS or rows16:
         while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
                and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
             splits *= 2
@@ -275,7 +285,7 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
     if rows <= split_max_rows(head_dim) and seq_kv >= SPLIT_MIN_KV:
         rpw = split_rows_per_workgroup(rows, head_dim)
         base = _cdiv(rows, rpw) * num_kv_heads * batch
-        splits = split_count(base, seq_kv, cu_count, rpw, head_dim)
+        splits = split_count(base, seq_kv, cu_count, rpw, head_dim, rows16=rows <= DEC16_ROWS)
         return Route("split", splits, base * splits)
     ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal)
     # Key chunks, against the better of the plain and the block-split single pass.

@@ -1,10 +1,11 @@
-"""GPU parity of the 16-row split-KV first pass (gqa_decode16_kernel: at
-head_dim 128 every (b, kv head) with at most 16 packed query rows) against
-the CPU oracle: every packed-row count 1-16 through group sizes and query
-lengths, odd groups (a position's heads split across lanes of different
-lane groups), fp16, non-causal, the LSE side output, rows with no visible
-key, an empty cache, and paged caches of 16- and 32-key blocks (one
-descriptor per wave and tile) with ragged sequence lengths."""
+"""GPU parity of the 16-row split-KV first pass (gqa_decode16_kernel: every
+(b, kv head) with at most 16 packed query rows, at head_dim 128 and 64)
+against the CPU oracle: every packed-row count 1-16 through group sizes and
+query lengths, odd groups (a position's heads split across lanes of
+different lane groups), fp16, non-causal, the LSE side output, rows with no
+visible key, an empty cache, and paged caches of 8- to 64-key blocks (one
+descriptor per instruction, per wave and tile, or per tile) with ragged
+sequence lengths."""
 from __future__ import annotations
 
 import numpy as np
@@ -31,13 +32,14 @@ def _need_gpu():
     (8, 8, 16), (16, 8, 8),                  # MHA with 16 positions, G = 2 with 8
 ])
 @pytest.mark.parametrize("S", [3, 16])
-def test_decode16_rows(Hq, Hkv, sq, S):
+@pytest.mark.parametrize("D", [128, 64])
+def test_decode16_rows(Hq, Hkv, sq, S, D):
     from gqa_kernels.gqa_split import split_kv_forward
     from oracle.gqa_oracle import gqa_lse
     skv = 64 * 7 * S + 29  # ragged last tile; S * 7 tiles
-    q, k, v = make_inputs(1, Hq, Hkv, sq, skv, 128, torch.bfloat16, seed=Hq * 31 + sq + S, device=DEV)
+    q, k, v = make_inputs(1, Hq, Hkv, sq, skv, D, torch.bfloat16, seed=Hq * 31 + sq + S, device=DEV)
     assert (Hq // Hkv) * sq <= 16
-    print(f"decode16 Hq={Hq} Hkv={Hkv} sq={sq} S={S}", flush=True)
+    print(f"decode16 Hq={Hq} Hkv={Hkv} sq={sq} S={S} D={D}", flush=True)
     o, lse = split_kv_forward(q, k, v, True, S, return_lse=True)
     torch.cuda.synchronize()
     assert_close(o, oracle(q, k, v), BASELINE_TOL[torch.bfloat16], f"rows {Hq // Hkv * sq}")
@@ -46,18 +48,20 @@ def test_decode16_rows(Hq, Hkv, sq, S):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_decode16_fp16(causal):
+@pytest.mark.parametrize("D", [128, 64])
+def test_decode16_fp16(causal, D):
     from gqa_kernels import gqa_flash_attn
-    q, k, v = make_inputs(2, 32, 8, 1, 5000, 128, torch.float16, scale=0.1, seed=3, device=DEV)
+    q, k, v = make_inputs(2, 32, 8, 1, 5000, D, torch.float16, scale=0.1, seed=3, device=DEV)
     o = gqa_flash_attn(q, k, v, causal=causal)
     torch.cuda.synchronize()
-    assert_close(o, oracle(q, k, v, causal=causal), REF_TOL[torch.float16], f"fp16 causal={causal}")
+    assert_close(o, oracle(q, k, v, causal=causal), REF_TOL[torch.float16], f"fp16 causal={causal} D={D}")
 
 
-def test_decode16_rows_without_keys_and_empty_cache():
+@pytest.mark.parametrize("D", [128, 64])
+def test_decode16_rows_without_keys_and_empty_cache(D):
     from gqa_kernels.gqa_split import split_kv_forward
     # seq_q > seq_kv under causal: positions 0..sq-skv-1 see no key (NaN rows).
-    q, k, v = make_inputs(1, 16, 4, 4, 2, 128, torch.bfloat16, seed=9, device=DEV)
+    q, k, v = make_inputs(1, 16, 4, 4, 2, D, torch.bfloat16, seed=9, device=DEV)
     o = split_kv_forward(q, k, v, True, 2)
     torch.cuda.synchronize()
     ref = oracle(q, k, v)
@@ -66,21 +70,23 @@ def test_decode16_rows_without_keys_and_empty_cache():
     assert nan.any() and np.array_equal(np.isnan(got), nan)
     np.testing.assert_allclose(got[~nan], ref[~nan], rtol=0, atol=2e-2)
     # An empty cache: zero rows.
-    q, k, v = make_inputs(1, 32, 8, 1, 0, 128, torch.bfloat16, seed=9, device=DEV)
+    q, k, v = make_inputs(1, 32, 8, 1, 0, D, torch.bfloat16, seed=9, device=DEV)
     o = split_kv_forward(q, k, v, True, 4)
     torch.cuda.synchronize()
     assert torch.count_nonzero(o).item() == 0
 
 
-@pytest.mark.parametrize("block_size,layout", [(16, "NHD"), (32, "HND"), (32, "NHD")])
+@pytest.mark.parametrize("block_size,layout,D", [(16, "NHD", 128), (32, "HND", 128), (32, "NHD", 128),
+                                                 (8, "NHD", 64), (16, "NHD", 64), (32, "HND", 64), (64, "NHD", 64),
+                                                 (64, "HND", 64)])
 @pytest.mark.parametrize("sq", [1, 4])
-def test_decode16_paged_medium_blocks(block_size, layout, sq):
+def test_decode16_paged_medium_blocks(block_size, layout, D, sq):
     # Pages of 16-32 keys: each wave loads 16 consecutive rows of a tile
     # (one page); ragged lengths end inside a wave's share and inside a
     # page; unused slots hold NaN and must never be read.
     from gqa_kernels.paged import paged_attention
     from oracle.gqa_oracle import paged_reference
-    B, Hq, Hkv, D = 3, 32, 8, 128
+    B, Hq, Hkv = 3, 32, 8
     lens = [4096 + 7, 1000, 70]
     g = torch.Generator(device="cpu").manual_seed(block_size + sq)
     maxb = max(-(-n // block_size) for n in lens)
@@ -107,7 +113,7 @@ def test_decode16_paged_medium_blocks(block_size, layout, sq):
     else:
         kcv, vcv = kc, vc
     q = torch.randn(B, Hq, sq, D, generator=g).to(torch.bfloat16)
-    print(f"decode16 paged bs={block_size} {layout} sq={sq}", flush=True)
+    print(f"decode16 paged bs={block_size} {layout} D={D} sq={sq}", flush=True)
     o = paged_attention(q.to(DEV), kcv.to(DEV), vcv.to(DEV), table.to(DEV),
                         torch.tensor(lens, dtype=torch.int32, device=DEV), True, max_seq_len=max(lens))
     torch.cuda.synchronize()
