@@ -521,7 +521,7 @@ CONFIGS = (
 # 128-token chunk (the single pass over key chunks), both against 131072 keys;
 # then the headline prefill and decode in fp16 (the other input type the
 # reference accepts, dispatch.py:18) and with the LSE side output
-# (return_lse=True).  Optional trailing fields: dtype ("bf16" default,
+# (return_lse=True), and the decode at head_dim 64 (dispatch.py:32).  Optional trailing fields: dtype ("bf16" default,
 # "fp16") and return_lse.
 EXTRAS = (
     ("verify 16 x 131072", 1, 32, 8, 16, 131072, "hbm", 128),
@@ -530,6 +530,7 @@ EXTRAS = (
     ("decode 131072 fp16", 1, 32, 8, 1, 131072, "hbm", 128, "fp16"),
     ("prefill 16384 return_lse", 1, 32, 8, 16384, 16384, "mfma", 128, "bf16", True),
     ("decode 131072 return_lse", 1, 32, 8, 1, 131072, "hbm", 128, "bf16", True),
+    ("decode 131072 head_dim 64", 1, 32, 8, 1, 131072, "hbm", 64),
 )
 # Untimed calls of every config beyond the headline run for at least this
 # long before its timed calls (its inputs were just drawn on the host, the
