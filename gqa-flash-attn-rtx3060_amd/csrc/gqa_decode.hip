@@ -659,15 +659,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int NI = ST::NI;    // LDS-DMA instructions per wave per K (or V) tile
   constexpr int NKS = D / 32;   // k-steps of S^T
   constexpr int NDB = D / 64;   // 16-dim blocks of O^T per wave
+  // Keys per step: 64 at head_dim 128; 128 at head_dim 64 (two 64-row
+  // sub-tiles per stage), so that a step moves the same 32 KiB of K and V.
+  constexpr int TK = D == 64 ? 128 : 64;
+  constexpr int NKB = TK / 16;  // 16-key blocks of S^T per step
+  constexpr int NSUB = TK / 64;
   // The V swizzle (chunk XOR) of tile row r: a function of r & 7.
   auto sv16 = [](int r) { return D == 128 ? 2 * (r & 7) : (r & 6); };
   // LDS as gqa_decode_kernel: two stages (64 KiB at head_dim 128, two
   // workgroups per CU; a third stage for grids of one workgroup per CU
   // measured slower at 8K-32K keys), reused by the fused combine.
-  __shared__ __attribute__((aligned(1024))) char lds_a_k0[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_b_v0[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_c_k1[ST::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds_d_v1[ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_a_k0[NSUB * ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_b_v0[NSUB * ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_c_k1[NSUB * ST::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds_d_v1[NSUB * ST::kTileBytes];
   __shared__ int s_last;
 
   const Dims& dm = p.dm;
@@ -700,7 +705,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int pos_hi = min(sq - 1, 15 / dm.G);
   if (dm.causal) c1 = min(c1, pos_hi + (skv - sq) + 1);
   const int nk = max(c1 - c0, 0);
-  const int ntiles = (nk + 63) >> 6;
+  const int ntiles = (nk + TK - 1) / TK;
   const int qpos_lo = skv - sq;
 
   const uint32_t kssb = (uint32_t)(2 * p.k.ss), vssb = (uint32_t)(2 * p.v.ss);
@@ -727,8 +732,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint32_t koff =
       (uint32_t)(lrow * kssb) + 16u * (uint32_t)((lane % CPR) ^ ST::gk((wave * ST::RPI + lrow) & 15));
   const uint32_t voff = (uint32_t)(lrow * vssb) + 16u * (uint32_t)((lane % CPR) ^ sv16(wave * ST::RPI + lrow));
-  auto issue = [&](int it, char* kst, char* vst) {
-    const int j = tile_rel(it) * 64;
+  // Loads of the 64 rows from key j of the chunk into kst / vst.
+  auto issue64 = [&](int j, char* kst, char* vst) {
     if constexpr (KV == 0) {
       issue_tile_dma<D, kDmaStream>(kst, rk, (uint32_t)j * kssb, kssb, koff, wave);
       issue_tile_dma<D, kDmaStream>(vst, rv, (uint32_t)j * vssb, vssb, voff, wave);
@@ -787,6 +792,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
+  // Step `it` (TK keys from tile_rel(it) * TK): NSUB sub-tiles of 64 rows.
+  auto issue = [&](int it, char* kst, char* vst) {
+    const int j = tile_rel(it) * TK;
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) issue64(j + 64 * sub, kst + sub * ST::kTileBytes, vst + sub * ST::kTileBytes);
+  };
 
   // Loads in issue order: tile 0, Q (only lanes of valid rows touch memory:
   // an invalid lane's offset lies past the query group's descriptor and
@@ -805,7 +816,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   issue(1, lds_c_k1, lds_d_v1);
   // Tile 0 and Q have landed (tile 1 may still be in flight).
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NI));
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NI * NSUB));
 
   // LDS read offsets.  K: row 16 kb + i16, chunk 4 ks + lg (16 lanes of a
   // lane group read 16 rows at distinct swizzled chunks: conflict-free).
@@ -848,26 +859,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if ((it & 3) == 0) set_prio(it);
     // This wave's loads of tile it have landed (those of tile it + 1 may
     // still be in flight); after the barrier, every wave's have.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LAST ? 0 : 2 * NI));
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LAST ? 0 : 2 * NI * NSUB));
     phase_barrier();
 
-    // S^T for the 64 keys: four 16-key blocks, NKS k-steps each.
-    f32x4 sc[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
-    {
-      u32x4 opk[4 * NKS];
+    // S^T for the TK keys: NKB 16-key blocks, NKS k-steps each.
+    f32x4 sc[NKB];
 #pragma unroll
-      for (int j = 0; j < 4 * NKS; ++j)
+    for (int kb = 0; kb < NKB; ++kb) sc[kb] = f32x4{};
+    {
+      u32x4 opk[NKB * NKS];
+#pragma unroll
+      for (int j = 0; j < NKB * NKS; ++j)
         opk[j] = *reinterpret_cast<const u32x4*>(ck + (j / NKS) * 16 * (2 * D) + ka[j % NKS]);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) sc[kb] = E::mfma16(opk[kb * NKS + ks], qreg[ks], sc[kb]);
+        for (int kb = 0; kb < NKB; ++kb) sc[kb] = E::mfma16(opk[kb * NKS + ks], qreg[ks], sc[kb]);
     }
-    const int key0 = c0 + tile_rel(it) * 64;
-    const bool need_mask = (key0 + 64 > c1) || (dm.causal && key0 + 63 > qpos_lo);
+    const int key0 = c0 + tile_rel(it) * TK;
+    const bool need_mask = (key0 + TK > c1) || (dm.causal && key0 + TK - 1 > qpos_lo);
     if (need_mask) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int key = key0 + 16 * kb + 4 * lg + v;
@@ -877,24 +890,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     // Exact online softmax (gqa_split.py:92-101) in exp2 units; a row with
     // no visible key so far keeps m = -inf and uses 0 as reference.
-    const float t0 = vmax3(sc[0][0], sc[0][1], sc[0][2]), t1 = vmax3(sc[0][3], sc[1][0], sc[1][1]);
-    const float t2 = vmax3(sc[1][2], sc[1][3], sc[2][0]), t3 = vmax3(sc[2][1], sc[2][2], sc[2][3]);
-    const float t4 = vmax3(sc[3][0], sc[3][1], sc[3][2]);
-    const float mx = xhalf_max(xquad_max(fmaxf(vmax3(t0, t1, t2), vmax3(t3, t4, sc[3][3]))));
+    float mx;
+    if constexpr (NKB == 4) {
+      const float t0 = vmax3(sc[0][0], sc[0][1], sc[0][2]), t1 = vmax3(sc[0][3], sc[1][0], sc[1][1]);
+      const float t2 = vmax3(sc[1][2], sc[1][3], sc[2][0]), t3 = vmax3(sc[2][1], sc[2][2], sc[2][3]);
+      const float t4 = vmax3(sc[3][0], sc[3][1], sc[3][2]);
+      mx = xhalf_max(xquad_max(fmaxf(vmax3(t0, t1, t2), vmax3(t3, t4, sc[3][3]))));
+    } else {
+      float tb[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) tb[kb] = fmaxf(vmax3(sc[kb][0], sc[kb][1], sc[kb][2]), sc[kb][3]);
+#pragma unroll
+      for (int w = NKB / 2; w >= 1; w /= 2)
+#pragma unroll
+        for (int kb = 0; kb < w; ++kb) tb[kb] = fmaxf(tb[kb], tb[kb + w]);
+      mx = xhalf_max(xquad_max(tb[0]));
+    }
     const float m_new = fmaxf(m_run, mx);
     const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
     const float alpha = fast_exp2((m_run - m_use) * c);
     const float nmc = -m_use * c;
-    float pv[4][4];
+    float pv[NKB][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int v = 0; v < 4; ++v) pv[kb][v] = fast_exp2(__builtin_fmaf(sc[kb][v], c, nmc));
-    const float rs = ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) + ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3])) +
-                     (((pv[2][0] + pv[2][1]) + (pv[2][2] + pv[2][3])) + ((pv[3][0] + pv[3][1]) + (pv[3][2] + pv[3][3])));
-    u32x4 pk[2];
+    float rs;
+    if constexpr (NKB == 4) {
+      rs = ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) + ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3])) +
+           (((pv[2][0] + pv[2][1]) + (pv[2][2] + pv[2][3])) + ((pv[3][0] + pv[3][1]) + (pv[3][2] + pv[3][3])));
+    } else {
+      float tb[NKB];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int kb = 0; kb < NKB; ++kb) tb[kb] = (pv[kb][0] + pv[kb][1]) + (pv[kb][2] + pv[kb][3]);
+#pragma unroll
+      for (int w = NKB / 2; w >= 1; w /= 2)
+#pragma unroll
+        for (int kb = 0; kb < w; ++kb) tb[kb] = tb[kb] + tb[kb + w];
+      rs = tb[0];
+    }
+    u32x4 pk[NKB / 2];
+#pragma unroll
+    for (int j = 0; j < NKB / 2; ++j)
       pk[j] = u32x4{E::pack2(pv[2 * j][0], pv[2 * j][1]), E::pack2(pv[2 * j][2], pv[2 * j][3]),
                     E::pack2(pv[2 * j + 1][0], pv[2 * j + 1][1]), E::pack2(pv[2 * j + 1][2], pv[2 * j + 1][3])};
     l_run = l_run * alpha + rs;
@@ -902,11 +939,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
 
-    // O^T (this wave's dims) += V^T P^T over the 64 keys.
+    // O^T (this wave's dims) += V^T P^T over the TK keys.
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NKB / 2; ++j) {
         const u32x2 lo = ld_tr(cv + vb[db] + (32 * j) * (2 * D));
         const u32x2 hi = ld_tr(cv + vb[db] + (32 * j + 16) * (2 * D));
         acc[db] = E::mfma16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[j], acc[db]);
@@ -979,9 +1016,10 @@ bool decode_kernel_fits(const SplitParams& p) {
   // Paged: whole LDS-DMA instructions (512 / D rows) in a page, and
   // 64-key-aligned chunks (so a tile lies in a page of >= 64 keys).
   if (paged && ((1 << p.block_shift) < 512 / D || (p.chunk & 63) != 0)) return false;
-  // 32-bit descriptor offsets: (contiguous) a chunk plus a tile of K and V
-  // rows, (paged) a tile of rows; the whole accumulator workspace.
-  const int64_t span = paged ? 64 : (int64_t)p.chunk + 64;
+  // 32-bit descriptor offsets: (contiguous) a chunk plus the padding step
+  // past it (two steps of 64 keys at head_dim 128, of 128 at 64), (paged) a
+  // 64-row sub-tile; the whole accumulator workspace.
+  const int64_t span = paged ? 64 : (int64_t)p.chunk + (D == 64 ? 256 : 128);
   if (span * p.k.ss * 2 >= ((int64_t)1 << 31) || span * p.v.ss * 2 >= ((int64_t)1 << 31)) return false;
   const int64_t acc_bytes = (int64_t)p.dm.B * p.dm.Hq * p.dm.Sq * p.splits * D * 4;
   // ... and a kv head's query group (its G heads x Sq rows).

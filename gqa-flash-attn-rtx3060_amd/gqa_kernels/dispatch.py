@@ -56,11 +56,14 @@ SPLIT_MIN_TILES = 1
 # runs two per CU at once; one round of workgroups measured fastest).
 SPLIT_WG_PER_CU = 2
 # Packed rows per kv head up to which head_dim 64 also runs the 16-row
-# LDS-DMA first pass, and with it the head_dim-128 split count.  Measured on
-# MI355X (bf16, one token, G = 4, rotating K/V sets, us): 32768 keys 32
-# splits 17.3 / 64 18.2 (register-staged pass: 20.1 at 64), 131072 keys 32
-# 46.8 / 64 45.9 / 128 50.3 (47.9 at 64), B = 4 x 32768 8 46.7 / 16 46.0 /
-# 32 50.5, 8192 keys 32 10.9 / 64 10.7.
+# LDS-DMA first pass (in 128-key steps), and with it the head_dim-128 split
+# count with the doubling threshold counted in steps (SPLIT_WIDER_MIN_CHUNK
+# keys of 64-key steps = twice as many keys of 128-key steps).  Measured on
+# MI355X (bf16, one token unless noted, G = 4, rotating K/V sets, us):
+# 32768 keys 32 splits 16.7 / 64 18.1 (register-staged pass: 20.1 at 64),
+# 131072 keys 32 45.0 / 64 46.2 (47.9 at 64), B = 4 x 32768 8 45.1 / 16
+# 46.5, 4 tokens at 131072 keys 32 45.7 / 64 47.1, B = 16 x 8192 2 45.7 / 4
+# 46.5, 8192 keys 16 11.2 / 32 11.6.
 DEC16_ROWS = 16
 # Single pass with key-range split of the heaviest causal query blocks: only
 # considered while there are fewer than this many workgroups per CU, and
@@ -247,11 +250,12 @@ def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int, head_di
     target = SPLIT_WG_PER_CU * cu_count
     splits = 1
     if head_dim == 128 or rows_per_wg > SPLIT_WIDE_ROWS or rows16:
+        wider_min = SPLIT_WIDER_MIN_CHUNK * (2 if head_dim == 64 else 1)
         while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
                and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
             splits *= 2
         while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
-               and _cdiv(seq_kv, splits * 2) >= SPLIT_WIDER_MIN_CHUNK):
+               and _cdiv(seq_kv, splits * 2) >= wider_min):
             splits *= 2
         return splits
     while (base * splits < target and splits < _lib.GQA_MAX_SPLITS

@@ -57,10 +57,11 @@ _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 # Split sizing: a power of two split count that brings the first pass to a
 # number of workgroups per compute unit, every chunk keeping at least two
 # 128-key tiles.  Workgroups per CU: two for the register-staged first pass
-# (head_dim 64, pages of 1-2 keys); for the LDS-DMA first pass (head_dim
-# 128, pages of >= 4 keys) one, or four for a single-token step of a batch
-# of sequences over pages whose heads of a key are interleaved (token-major,
-# slot stride != head_dim).  Measured on MI355X (bf16, Hq = 32, Hkv = 8,
+# (head_dim 64 over more than 16 rows, pages of 1-2 keys, or 4 at head_dim
+# 64); for the LDS-DMA first pass (head_dim 128 with pages of >= 4 keys, and
+# head_dim 64 with at most 16 rows and pages of >= 8 keys) one, or four for
+# a single-token step of a batch of sequences over pages whose heads of a
+# key are interleaved (token-major, slot stride != head_dim).  Measured on MI355X (bf16, Hq = 32, Hkv = 8,
 # random block order, us): head-major 64-key pages, one token, 131072 keys
 # 32 / 64 splits 83.3 / 85.0, B = 4 x 32768 8 / 16 splits 81.0 / 84.6,
 # B = 16 x 8192 2 / 4 80.8 / 83.0, 16 tokens at 32768 keys 32 / 64 32.7 /
@@ -68,7 +69,11 @@ _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 # 89.1, B = 4 x 32768 8 / 16 / 32 splits 90.3 / 88.3 / 86.4, B = 16 x 8192
 # 2 / 4 / 8 90.3 / 92.2 / 88.9; several tokens, B = 2 x 32768 16 tokens
 # 16 / 32 / 64 splits 56.6 / 58.4 / 71.3, B = 8 x 8192 4 tokens 4 / 8 / 16
-# 49.8 / 50.6 / 51.1.
+# 49.8 / 50.6 / 51.1.  Head_dim 64, one token, fill / 2x / 4x the fill
+# count: head-major 64-key pages 131072 keys 44.7 / 45.8 / 46.5, B = 16 x
+# 8192 44.7 / 46.1 / 47.2; token-major 16-key pages 131072 keys 51.0 / 52.3
+# / 52.8, B = 4 x 32768 53.5 / 48.6 / 48.9, B = 16 x 8192 54.0 / 56.2 /
+# 49.5.
 _SPLIT_ROWS = 32
 _SPLIT_WG_PER_CU = 2
 _LDS_WG_PER_CU = 1
@@ -76,6 +81,7 @@ _LDS_WG_PER_CU_INTERLEAVED = 4
 _MIN_CHUNK = 256
 _SPLIT_MAX_ROWS = 64  # packed rows per kv head up to which the split-KV pass is used
 _SPLIT_MAX_ROWS_WIDE = 128  # ... at head_dim 128 with pages of >= 4 keys (128-row workgroups)
+_DEC16_ROWS = 16  # packed rows up to which head_dim 64 runs the LDS-DMA first pass
 
 _cu_lock = threading.Lock()
 _cu_counts: dict = {}
@@ -103,9 +109,10 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
                  cu_count: int, block_size: int = 64, head_dim: int = 128,
                  heads_interleaved: bool = False) -> int:
     """Split count for a paged call: the power of two that brings the first
-    pass to its target workgroups per compute unit (at head_dim 128 with
-    pages of >= 4 keys one, or four for a single-token step of a batch over
-    pages whose heads are interleaved; else two) while every chunk keeps at
+    pass to its target workgroups per compute unit (for the LDS-DMA first
+    pass — head_dim 128 with pages of >= 4 keys, head_dim 64 with at most 16
+    packed rows and pages of >= 8 keys — one, or four for a single-token
+    step of a batch over pages whose heads are interleaved; else two) while every chunk keeps at
     least 256 keys (pure function of the shapes and of ``heads_interleaved``:
     the cache's slot stride differs from head_dim).  With pages under 64 keys a chunk spans
     at most GQA_PAGED_CHUNK_PAGES pages (the slice of the block table a
@@ -114,7 +121,8 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
     rows = group * seq_q
     # Rows per first-pass workgroup: up to four 32-row blocks at head_dim 128
     # with pages of >= 4 keys (the LDS-DMA first pass), else one.
-    lds_pass = head_dim == 128 and block_size >= 4
+    lds_pass = ((head_dim == 128 and block_size >= 4)
+                or (head_dim == 64 and block_size >= 8 and rows <= _DEC16_ROWS))
     rpw = _SPLIT_ROWS
     if lds_pass and rows > _SPLIT_ROWS:
         rpw = 2 * _SPLIT_ROWS if rows <= 2 * _SPLIT_ROWS else 4 * _SPLIT_ROWS

@@ -244,7 +244,7 @@ def test_route_baseline_configs():
     # head_dim 64, one token (the 16-row first pass): the head_dim-128 count
     r = choose_route(1, 32, 8, 1, 8192, cu, True, 64)
     assert r.kind == "split" and r.splits == 32
-    assert choose_route(1, 32, 8, 1, 131072, cu, True, 64).splits == 64
+    assert choose_route(1, 32, 8, 1, 131072, cu, True, 64).splits == 32  # doubling from 4096-key chunks
     # head_dim 64 over more than 16 rows (the register-staged first pass):
     # two per CU with 128-key chunks
     r = choose_route(1, 32, 8, 8, 8192, cu, True, 64)

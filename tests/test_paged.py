@@ -227,8 +227,14 @@ def test_paged_splits():
     assert paged_splits(4, 32, 8, 1, 32768, 256) == 8
     assert paged_splits(4, 32, 8, 1, 32768, 256, heads_interleaved=True) == 32
     assert paged_splits(4, 32, 8, 4, 32768, 256, heads_interleaved=True) == 8
-    # head_dim 64 / pages of 1-2 keys (register-staged first pass): two per CU
-    assert paged_splits(1, 32, 8, 1, 131072, 256, head_dim=64) == 64
+    # head_dim 64 with at most 16 rows and pages of >= 8 keys: the LDS-DMA
+    # pass as well
+    assert paged_splits(1, 32, 8, 1, 131072, 256, head_dim=64) == 32
+    assert paged_splits(16, 32, 8, 1, 8192, 256, block_size=16, head_dim=64, heads_interleaved=True) == 8
+    # the register-staged first pass (head_dim 64 over more rows or pages of
+    # 4 keys, pages of 1-2 keys at head_dim 128): two per CU
+    assert paged_splits(1, 32, 8, 8, 131072, 256, head_dim=64) == 64
+    assert paged_splits(1, 32, 8, 1, 131072, 256, block_size=4, head_dim=64) == 64
     assert paged_splits(1, 32, 8, 1, 131072, 256, block_size=2) == 64
     assert paged_splits(64, 32, 8, 1, 4096, 256) == 1
     assert paged_splits(1, 32, 8, 1, 300, 256) == 1
