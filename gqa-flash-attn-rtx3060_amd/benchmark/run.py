@@ -22,6 +22,7 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import os
 import statistics
 import subprocess
 import sys
@@ -227,6 +228,9 @@ def markdown_table(rows):
 
 
 def _commit():
+    # A copy of the tree without git metadata can name its commit.
+    if os.environ.get("GQA_COMMIT"):
+        return os.environ["GQA_COMMIT"][:7]
     try:
         return subprocess.check_output(["git", "rev-parse", "--short=7", "HEAD"], cwd=HERE,
                                        stderr=subprocess.DEVNULL).decode().strip()
