@@ -104,7 +104,7 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
   // host bounds its size to 32-bit offsets).
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
 
-  // Round 1: m and l into registers, then this thread's first batch of
+  // Step 1: m and l into registers, then this thread's first batch of
   // accumulators, all in flight together.
   float mreg[kDecMlPerThread], lreg[kDecMlPerThread];
 #pragma unroll
@@ -163,7 +163,7 @@ __device__ void decode_combine(const SplitParams& p, int b, int kvh, int rb, int
   }
   __syncthreads();
 
-  // Round 2 (and more only past kDecBatch splits per thread): a * acc.
+  // Step 2 (more load batches only past kDecBatch splits per thread): a * acc.
   for (bool first = true; it < n_work; it += 256, first = false) {
     if (!first) {
       item = it % items;
