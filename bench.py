@@ -297,7 +297,7 @@ def main() -> int:
                     help="minimum untimed time per config beyond the headline (0: the --warmup calls only; "
                          "for counter-collection runs)")
     ap.add_argument("--config", default=None,
-                    help="with --only configs: time only the BASELINE configs whose name starts with this")
+                    help="with --only configs (or extras): time only the configs (extra shapes) whose name starts with this")
     ap.add_argument("--only", choices=["prefill", "decode", "paged", "copy", "gemm", "chunked", "70b", "configs",
                                        "extras"],
                     default=None,
@@ -427,7 +427,7 @@ def main() -> int:
         result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup)
         result["extras"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup, table=EXTRAS)
     elif args.only == "extras":
-        result["extras"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup, table=EXTRAS)
+        result["extras"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup, only=args.config, table=EXTRAS)
     elif args.only in ("chunked", "70b"):
         result["configs"] = sweep(torch, gqa_flash_attn, args.steps, args.warmup,
                                   only={"chunked": "chunked", "70b": "70B"}[args.only])
