@@ -17,21 +17,22 @@
 // read transposed by ds_read_b64_tr_b16 (the single-pass kernel's layout,
 // gqa_lds.hpp).
 //
-// The 4 waves split the head dimension, not the keys: every wave computes
-// S^T = K Q^T for all 64 keys of a tile and the same exact online softmax
-// (the same instructions on the same data: bit-identical statistics in every
-// wave), and wave w accumulates O^T for dims [32w, 32w + 32).  At the end of
-// the chunk each wave stores its own 32 dims of the valid rows' partials —
-// no cross-wave merge.  With a decode group of 4 query rows most of each
-// S^T MFMA is padding; it runs hidden under the HBM stream.
+// The 4 waves of a workgroup split the keys and the head dimension.  RW = 1
+// (one 32-row block): waves 2k + h take keys [32k, 32k + 32) of every
+// 64-key tile (key group k) and dims [64h, 64h + 64), each running its own
+// exact online softmax over its keys; RW = 2 (33-64 packed rows per kv
+// head, e.g. verify steps of 9-16 tokens at G = 4): waves 2r + k take rows
+// [32r, 32r + 32) of the block, key group k, all 128 dims; RW = 4 (65-128
+// rows): wave r takes rows [32r, 32r + 32), all keys and dims.  At the end
+// of the chunk key group 1 hands its state to key group 0 through LDS,
+// which merges the two as the combine merges two splits and stores the
+// valid rows' partials of its dims.  (Splitting only the dims made every
+// wave of a row block compute the same scores and probabilities: 2 % more
+// time on the 70B decode shape.)  With a decode group of 4 query rows most
+// of each S^T MFMA is padding; it runs hidden under the HBM stream.
 //
-// Wide row blocks (RW = 2 or 4, for 33-64 or 65-128 packed rows per kv
-// head, e.g. verify steps of 9-16 or 17-32 tokens at G = 4): one workgroup
-// takes RW 32-row blocks, so the chunk's K/V stream once instead of once
-// per 32-row block.  RW = 2: waves 2h and 2h + 1 take rows [32h, 32h + 32)
-// of the block, each with 64 of the 128 dims; RW = 4: wave h takes rows
-// [32h, 32h + 32) with all 128 dims.  Partials and the fused combine stay
-// per 32-row block.
+// Wide row blocks (RW = 2 or 4) stream the chunk's K/V once instead of once
+// per 32-row block.  Partials and the fused combine stay per 32-row block.
 //
 // Fused combine (SplitParams::counters set): the last workgroup of each
 // (b, kv head, row block) to count its partial in combines all splits
@@ -244,13 +245,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6) & 3;
   const int i = lane & 31, hh = lane >> 5;
-  // This wave's 32-row block within the workgroup's (rh) and its NDB 32-dim
-  // blocks of O^T from db0: RW = 1, dim block `wave`; RW = 2, dim blocks
-  // 2 (wave & 1) and 2 (wave & 1) + 1; RW = 4, all four.
-  constexpr int NDB = RW;
+  // This wave's 32-row block within the workgroup's (rh), its key group kh
+  // and its NDB 32-dim blocks of O^T from db0.  The WPR waves of a row block
+  // are KS key groups (each takes 64 / KS keys of every tile with its own
+  // online softmax state; the groups' states are merged in LDS after the
+  // chunk) times DS dim groups: RW = 1, two key groups x two dim groups of
+  // 64 dims; RW = 2, two key groups of all 128 dims; RW = 4, one wave with
+  // all 128 dims.  Splitting the keys instead of only the dims spares the
+  // waves of a row block computing the same scores and probabilities twice.
   constexpr int WPR = 4 / RW;  // waves per 32-row block
+  constexpr int KS = WPR >= 2 ? 2 : 1;
+  constexpr int DS = WPR / KS;
+  constexpr int NDB = 4 / DS;
+  constexpr int NMB = 2 / KS;  // 32-key blocks of a tile per wave
   const int rh = wave / WPR;
-  const int db0 = (wave % WPR) * RW;
+  const int kh = (wave % WPR) % KS;
+  const int db0 = ((wave % WPR) / KS) * NDB;
 
   const int n_wblk = (p.n_rblk + RW - 1) / RW;
   const int total = dm.B * dm.Hkv * n_wblk * p.splits;
@@ -472,23 +482,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(LAST ? 0 : 2 * NI));
     phase_barrier();
 
-    // S^T for the 64 keys: two 32-key blocks, NKS k-steps each.
-    f32x16 sc[2] = {f32x16{}, f32x16{}};
+    // S^T for this wave's keys of the tile: NMB 32-key blocks (blocks
+    // kh * NMB + mb of the tile), NKS k-steps each.
+    f32x16 sc[NMB] = {};
     {
-      u32x4 opk[2 * NKS];
+      u32x4 opk[NMB * NKS];
 #pragma unroll
-      for (int j = 0; j < 2 * NKS; ++j) opk[j] = *reinterpret_cast<const u32x4*>(ck + (j & 1) * 32 * (2 * D) + ka[j >> 1]);
+      for (int j = 0; j < NMB * NKS; ++j)
+        opk[j] = *reinterpret_cast<const u32x4*>(ck + (kh * NMB + j % NMB) * 32 * (2 * D) + ka[j / NMB]);
 #pragma unroll
-      for (int j = 0; j < 2 * NKS; ++j) sc[j & 1] = E::mfma(opk[j], qreg[j >> 1], sc[j & 1]);
+      for (int j = 0; j < NMB * NKS; ++j) sc[j % NMB] = E::mfma(opk[j], qreg[j / NMB], sc[j % NMB]);
     }
     const int key0 = c0 + tile_rel(it) * 64;
     const bool need_mask = (key0 + 64 > c1) || (dm.causal && key0 + 63 > qpos_lo);
     if (need_mask) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int key = key0 + 32 * mb + key_of(v, hh);
+          const int key = key0 + 32 * (kh * NMB + mb) + key_of(v, hh);
           const bool off = key >= c1 || (dm.causal && key > qpos);
           sc[mb][v] = off ? -__builtin_inff() : sc[mb][v];
         }
@@ -496,24 +508,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Exact online softmax (gqa_split.py:92-101) in exp2 units; a row with
     // no visible key so far keeps m = -inf and uses 0 as reference, so its
     // probabilities are 0, never NaN.
-    float m1[11];
+    float mx;
+    if constexpr (NMB == 2) {
+      float m1[11];
 #pragma unroll
-    for (int k = 0; k < 10; ++k) {
-      const int i0 = 3 * k, i1 = 3 * k + 1, i2 = 3 * k + 2;
-      m1[k] = vmax3(sc[i0 >> 4][i0 & 15], sc[i1 >> 4][i1 & 15], sc[i2 >> 4][i2 & 15]);
+      for (int k = 0; k < 10; ++k) {
+        const int i0 = 3 * k, i1 = 3 * k + 1, i2 = 3 * k + 2;
+        m1[k] = vmax3(sc[i0 >> 4][i0 & 15], sc[i1 >> 4][i1 & 15], sc[i2 >> 4][i2 & 15]);
+      }
+      m1[10] = vmax3(sc[NMB - 1][14], sc[NMB - 1][15], sc[NMB - 1][15]);
+      const float n0 = vmax3(m1[0], m1[1], m1[2]), n1 = vmax3(m1[3], m1[4], m1[5]);
+      const float n2 = vmax3(m1[6], m1[7], m1[8]), n3 = vmax3(m1[9], m1[10], m1[10]);
+      mx = xhalf_max(vmax3(vmax3(n0, n1, n2), n3, n3));
+    } else {
+      float m1[5];
+#pragma unroll
+      for (int k = 0; k < 5; ++k) m1[k] = vmax3(sc[0][3 * k], sc[0][3 * k + 1], sc[0][3 * k + 2]);
+      mx = xhalf_max(vmax3(vmax3(m1[0], m1[1], m1[2]), vmax3(m1[3], m1[4], sc[0][15]), sc[0][15]));
     }
-    m1[10] = vmax3(sc[1][14], sc[1][15], sc[1][15]);
-    const float n0 = vmax3(m1[0], m1[1], m1[2]), n1 = vmax3(m1[3], m1[4], m1[5]);
-    const float n2 = vmax3(m1[6], m1[7], m1[8]), n3 = vmax3(m1[9], m1[10], m1[10]);
-    const float mx = xhalf_max(vmax3(vmax3(n0, n1, n2), n3, n3));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
     const float alpha = fast_exp2((m_run - m_use) * c);
     const float nmc = -m_use * c;
-    u32x4 pk[2][2];
+    u32x4 pk[NMB][2];
     float rs = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < NMB; ++mb) {
       float pv[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) pv[v] = fast_exp2(__builtin_fmaf(sc[mb][v], c, nmc));
@@ -533,13 +553,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[d][v] *= alpha;
 
-    // O^T (this wave's dims) += V^T P^T over the 64 keys.
+    // O^T (this wave's dims) += V^T P^T over this wave's keys.
 #pragma unroll
     for (int d = 0; d < NDB; ++d)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2 * NMB; ++j) {
         const int mb = j >> 1, kk = j & 1;
-        const int ro = (32 * mb + 16 * kk) * (2 * D);
+        const int ro = (32 * (kh * NMB + mb) + 16 * kk) * (2 * D);
         const u32x2 lo = ld_tr(cv + vb[d] + ro);
         const u32x2 hi = ld_tr(cv + vb[d] + ro + 4 * (2 * D));
         acc[d] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[mb][kk], acc[d]);
@@ -571,10 +591,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // stages.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
+  if constexpr (KS == 2) {
+    // Key group 1 hands its state (the same lanes' rows and dims) to key
+    // group 0 through LDS, lane-major; group 0 merges it as the combine
+    // merges two splits (gqa_split.py:137-144), a group with no visible key
+    // (m = -inf, l = 0, acc = 0) adding nothing.  Pair (row block, dim
+    // group) g uses stage arrays 2 g (accumulators, NDB * 4 KiB) and 2 g + 1
+    // (m, l).
+    const int pair = wave / KS;
+    float* xa = reinterpret_cast<float*>(pair == 0 ? lds_a_k0 : lds_c_k1);
+    float* xm = reinterpret_cast<float*>(pair == 0 ? lds_b_v0 : lds_d_v1);
+    __syncthreads();  // every wave is done with the stages
+    if (kh == 1) {
+#pragma unroll
+      for (int d = 0; d < NDB; ++d)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) xa[(d * 16 + v) * 64 + lane] = acc[d][v];
+      xm[lane] = m_run;
+      xm[64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (kh == 0) {
+      const float m1 = xm[lane], l1 = xm[64 + lane];
+      const float mm = fmaxf(m_run, m1);
+      const float mu = (mm == -__builtin_inff()) ? 0.f : mm;
+      const float a0 = fast_exp2((m_run - mu) * c), a1 = fast_exp2((m1 - mu) * c);
+#pragma unroll
+      for (int d = 0; d < NDB; ++d)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[d][v] = __builtin_fmaf(acc[d][v], a0, xa[(d * 16 + v) * 64 + lane] * a1);
+      l_run = __builtin_fmaf(l_run, a0, l1 * a1);
+      m_run = mm;
+    }
+    __syncthreads();  // the stages are free again (the fused combine reuses them)
+  }
+
   // This wave's dims of the valid rows' partials: lane (i, hh) holds dims
-  // 32 * (db0 + d) + 8 * j + 4 * hh + 0..3 in acc[d][4j .. 4j + 3].
+  // 32 * (db0 + d) + 8 * j + 4 * hh + 0..3 in acc[d][4j .. 4j + 3].  With
+  // two key groups, group 0 holds the merged state.
   const float l_tot = xhalf_sum(l_run);
-  if (valid) {
+  if (valid && kh == 0) {
     const int64_t row = (((int64_t)b * dm.Hq + head) * dm.Sq + pos) * p.splits + s;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.ws_acc, 0xFFFFFFF0u);
 #pragma unroll
