@@ -76,17 +76,31 @@ FWD_SPLIT_GAIN = 0.05
 # measured split counts of causal prefill at 1024 and 2048 tokens (best
 # measured: 8 of 16 blocks, -18 %; 8 of 32, -10 %; none at 4096).
 FWD_ITEM_OVERHEAD = 8
+# Added to each half of a split block in the persistent kernel's model:
+# the exchange of its fp32 partial state (fitted to measured split counts
+# at 512-3072 tokens, B = 1-5; the one-workgroup-per-item form at head_dim
+# 64 measured best without it).
+FWD_MERGE_OVERHEAD = 1
 FWD_TILE = 64
+# The persistent single pass claims work dynamically only with at least this
+# many items per workgroup (kFwdDynMinItemsPerWg, gqa_params.hpp); below it
+# every workgroup takes a fixed list (gqa_fwd.hip item_at: XCD x's
+# contiguous item range dealt to its workgroups round by round in snake
+# order), which the run-time model then follows.
+FWD_DYN_MIN_ITEMS_PER_WG = 8
 # Key chunks (single pass over kv_splits key ranges per query block, then
 # the split-KV combine): considered when there are fewer query blocks than
 # compute units.  Per-item overhead (first loads, partial store) in tile
 # steps; a tile step of the single pass takes ~1.65 us on MI355X, the
 # combine launch ~3 us plus its read of the fp32 partials at ~5 TB/s.
-CHUNK_ITEM_OVERHEAD = 8
+CHUNK_ITEM_OVERHEAD = 12
 CHUNK_MIN_TILES = 4
 TILE_STEP_US = 1.65
 COMBINE_LAUNCH_US = 3.0
 COMBINE_BYTES_PER_US = 5.0e6
+# Passes over the fp32 partials charged to the key-chunk route: written by
+# the first pass, read back by the combine (fitted: 1.5).
+CHUNK_PARTIAL_PASSES = 1.5
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 
@@ -115,39 +129,49 @@ def _fwd_block_tiles(n_mblk: int, block_m: int, seq_q: int, seq_kv: int, causal:
     return out
 
 
-def fwd_split_makespan(tiles, n_split: int, n_bh: int, cu_count: int, causal: bool = True) -> float:
+def fwd_split_makespan(tiles, n_split: int, n_bh: int, cu_count: int, causal: bool = True,
+                       persistent: bool = True) -> float:
     """Modelled run time (tile steps) of the single pass with the n_split
     heaviest blocks split: work items in the kernel's order (per (b, kv
     head): upper halves of the split blocks, then every block heavy-first
-    with split blocks as their lower halves), each XCD (cu_count / 8 CUs)
-    taking its contiguous share of items, each CU the next item when free."""
+    with split blocks as their lower halves), scheduled as _list_makespan
+    describes (`persistent`: the head_dim-128 kernel over contiguous K/V)."""
     n = len(tiles)
     order = list(range(n - 1, -1, -1)) if causal else list(range(n))
-    items = [tiles[n - 1 - i] - tiles[n - 1 - i] // 2 for i in range(n_split)]
+    mo = FWD_MERGE_OVERHEAD if persistent else 0
+    items = [tiles[n - 1 - i] - tiles[n - 1 - i] // 2 + mo for i in range(n_split)]
     for pid in order:
-        items.append(tiles[pid] // 2 if pid >= n - n_split else tiles[pid])
-    per_bh = len(items)
-    total = per_bh * n_bh
-    q, r = divmod(total, 8)
-    per_xcd = max(1, cu_count // 8)
-    worst = 0.0
-    for x in range(8):
-        lo = x * q + min(x, r)
-        heap = [0.0] * per_xcd
-        for w in range(lo, lo + q + (1 if x < r else 0)):
-            heapq.heapreplace(heap, heap[0] + items[w % per_bh] + FWD_ITEM_OVERHEAD)
-        worst = max(worst, max(heap))
-    return worst
+        items.append(tiles[pid] // 2 + mo if pid >= n - n_split else tiles[pid])
+    return _list_makespan([c + FWD_ITEM_OVERHEAD for c in items] * n_bh, cu_count, persistent)
 
 
-def _list_makespan(items, cu_count: int) -> float:
-    """Run time (tile steps) of `items` (costs in the persistent kernel's
-    order): each XCD takes its contiguous share, each of its CUs the next
-    item when free."""
+def _list_makespan(items, cu_count: int, persistent: bool = False) -> float:
+    """Run time (tile steps) of `items` (costs in the kernel's item order):
+    each XCD (cu_count / 8 CUs) takes its contiguous share.  The persistent
+    kernel with fewer than FWD_DYN_MIN_ITEMS_PER_WG items per workgroup
+    deals fixed lists: workgroup `slot` of XCD x takes items slot, 2 S - 1 -
+    slot, 2 S + slot, ... of the XCD's share (S workgroups on the XCD:
+    gqa_fwd.hip item_at).  Otherwise (the dynamic schedule, or one
+    workgroup per item) each CU takes the next item when free."""
     total = len(items)
+    n_wg = min(total, cu_count)
     q, r = divmod(total, 8)
-    per_xcd = max(1, cu_count // 8)
     worst = 0.0
+    if persistent and total < FWD_DYN_MIN_ITEMS_PER_WG * n_wg:
+        for x in range(8):
+            lo, cnt = x * q + min(x, r), q + (1 if x < r else 0)
+            slots = (n_wg - x + 7) >> 3
+            for slot in range(slots):
+                t, j = 0.0, 0
+                while True:
+                    e = j * slots + (slots - 1 - slot if j & 1 else slot)
+                    if e >= cnt:
+                        break
+                    t += items[lo + e]
+                    j += 1
+                worst = max(worst, t)
+        return worst
+    per_xcd = max(1, cu_count // 8)
     for x in range(8):
         lo = x * q + min(x, r)
         heap = [0.0] * per_xcd
@@ -167,8 +191,10 @@ def chunks_makespan(tiles, kv_splits: int, n_bh: int, cu_count: int, rows: int, 
     ct = max(1, -(-max(tiles) // kv_splits))
     order = list(range(n - 1, -1, -1)) if causal else list(range(n))
     per_bh = [min(ct, max(tiles[m] - c * ct, 0)) + CHUNK_ITEM_OVERHEAD for c in range(kv_splits) for m in order]
-    first = _list_makespan(per_bh * n_bh, cu_count)
-    combine_us = COMBINE_LAUNCH_US + rows * kv_splits * (head_dim + 2) * 4 / COMBINE_BYTES_PER_US
+    first = _list_makespan(per_bh * n_bh, cu_count, persistent=head_dim == 128)
+    # The fp32 partials are written by the first pass and read back by the
+    # combine launch, each at about COMBINE_BYTES_PER_US.
+    combine_us = COMBINE_LAUNCH_US + CHUNK_PARTIAL_PASSES * rows * kv_splits * (head_dim + 2) * 4 / COMBINE_BYTES_PER_US
     return first + combine_us / TILE_STEP_US
 
 
@@ -190,7 +216,7 @@ def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
         return 0
     tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, seq_kv, causal)
     if base is None:
-        base = fwd_split_makespan(tiles, 0, n_bh, cu_count, causal)
+        base = fwd_split_makespan(tiles, 0, n_bh, cu_count, causal, persistent=head_dim == 128)
     rows = batch * num_heads * seq_q
     best, best_s = base, 0
     s = 2
@@ -203,7 +229,7 @@ def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
 
 
 def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
-                     cu_count: int, causal: bool) -> int:
+                     cu_count: int, causal: bool, head_dim: int = 128) -> int:
     """Query blocks per (b, kv head) to run as two key halves (0: none).
 
     Only causal blocks differ in length; when there are few workgroups per
@@ -216,11 +242,12 @@ def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
     if not causal or n_mblk < 2 or n_mblk * n_bh >= FWD_SPLIT_MAX_WG_PER_CU * cu_count:
         return 0
     tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, seq_kv, causal)
-    base = fwd_split_makespan(tiles, 0, n_bh, cu_count)
+    persistent = head_dim == 128
+    base = fwd_split_makespan(tiles, 0, n_bh, cu_count, persistent=persistent)
     best, best_ns = base, 0
     for f in (0.25, 0.375, 0.5, 0.625, 0.75, 1.0):
         ns = max(1, min(n_mblk, round(n_mblk * f)))
-        t = fwd_split_makespan(tiles, ns, n_bh, cu_count)
+        t = fwd_split_makespan(tiles, ns, n_bh, cu_count, persistent=persistent)
         if t < best:
             best, best_ns = t, ns
     return best_ns if best <= (1.0 - FWD_SPLIT_GAIN) * base else 0
@@ -291,14 +318,14 @@ def choose_route(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_
         base = _cdiv(rows, rpw) * num_kv_heads * batch
         splits = split_count(base, seq_kv, cu_count, rpw, head_dim, rows16=rows <= DEC16_ROWS)
         return Route("split", splits, base * splits)
-    ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal)
+    ns = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal, head_dim)
     # Key chunks, against the better of the plain and the block-split single pass.
     # (Only from SPLIT_MIN_KV keys on, the length from which the reference
     # splits the key axis at all.)
     n_mblk = _cdiv(seq_q, max(1, FWD_ROWS // group))
     if n_mblk * num_kv_heads * batch < cu_count and seq_q > 0 and seq_kv >= SPLIT_MIN_KV:
         tiles = _fwd_block_tiles(n_mblk, max(1, FWD_ROWS // group), seq_q, seq_kv, causal)
-        base = fwd_split_makespan(tiles, ns, num_kv_heads * batch, cu_count, causal)
+        base = fwd_split_makespan(tiles, ns, num_kv_heads * batch, cu_count, causal, persistent=head_dim == 128)
         kc = choose_kv_chunks(batch, num_heads, num_kv_heads, seq_q, seq_kv, cu_count, causal, head_dim, base)
         if kc:
             return Route("chunks", kc, single_wgs * kc)

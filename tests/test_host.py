@@ -340,6 +340,73 @@ def test_fwd_split_choice():
     assert _fwd_block_tiles(2, 64, 128, 1000, False) == [16, 16]
 
 
+def test_fwd_split_static_schedule_model():
+    """With fewer than FWD_DYN_MIN_ITEMS_PER_WG items per workgroup the
+    persistent single pass deals each workgroup a fixed item list
+    (gqa_fwd.hip item_at); the run-time model's makespan is the heaviest of
+    those lists, re-derived here per workgroup id as the kernel does
+    (XCD = id % 8, slot = id / 8, snake rounds over the XCD's range)."""
+    import random
+    from gqa_kernels.dispatch import (FWD_DYN_MIN_ITEMS_PER_WG, FWD_ITEM_OVERHEAD, FWD_MERGE_OVERHEAD,
+                                      _fwd_block_tiles, fwd_split_makespan)
+    rng = random.Random(5)
+    for _ in range(40):
+        n_mblk = rng.randint(2, 40)
+        n_bh = rng.randint(1, 12)
+        cu = rng.choice([16, 24, 64, 256])
+        ns = rng.randint(0, n_mblk)
+        tiles = _fwd_block_tiles(n_mblk, 64, 64 * n_mblk, 64 * n_mblk, True)
+        items = [tiles[n_mblk - 1 - i] - tiles[n_mblk - 1 - i] // 2 + FWD_MERGE_OVERHEAD for i in range(ns)]
+        items += [tiles[m] // 2 + FWD_MERGE_OVERHEAD if m >= n_mblk - ns else tiles[m]
+                  for m in range(n_mblk - 1, -1, -1)]
+        total = len(items) * n_bh
+        n_wg = min(total, cu)
+        if total >= FWD_DYN_MIN_ITEMS_PER_WG * n_wg:
+            continue
+        q, r = divmod(total, 8)
+        worst = 0
+        for wg in range(n_wg):
+            x, slot = wg % 8, wg // 8
+            S = (n_wg - x + 7) // 8
+            lo, n = x * q + min(x, r), q + (1 if x < r else 0)
+            t, k = 0, 0
+            while True:
+                e = k * S + (S - 1 - slot if k % 2 else slot)
+                if e >= n:
+                    break
+                t += items[(lo + e) % len(items)] + FWD_ITEM_OVERHEAD
+                k += 1
+            worst = max(worst, t)
+        assert fwd_split_makespan(tiles, ns, n_bh, cu) == worst
+
+
+def test_fwd_split_measured_choices():
+    # Causal prefill on one MI355X (us, the route taken vs the alternative):
+    # G = 4, B = 2 x 1536 tokens 56.0 unsplit -> 49.3 with 6 blocks split;
+    # B = 4 x 768 40.5 -> 35.1 with 4; B = 5 x 512 unsplit 27.9 vs 35.3
+    # with 4 split.
+    from gqa_kernels.dispatch import choose_route
+    assert choose_route(2, 32, 8, 1536, 1536, 256, True).fwd_split > 0
+    assert choose_route(4, 32, 8, 768, 768, 256, True).fwd_split > 0
+    assert choose_route(5, 32, 8, 512, 512, 256, True).fwd_split == 0
+    # Short chunks against short caches (the fp32 partials of key chunks
+    # cost more than the chunks save): 512 new tokens over 2048 keys, key
+    # chunks 43.0 us vs the single pass with every block split 32.1 (head
+    # dim 64: 45.3 vs 25.9); 128 x 2048 at B = 4 42.0 vs 33.8.
+    for D in (128, 64):
+        r = choose_route(1, 32, 8, 512, 2048, 256, True, D)
+        assert r.kind == "single" and r.fwd_split == 8
+    assert choose_route(4, 32, 8, 128, 2048, 256, True).kind == "single"
+    # Few query blocks against long caches keep the key chunks: 128 x 131072
+    # 238 us in 16 chunks vs 1068 single; 64 x 8192 29.1 in 16 vs 81.2.
+    assert choose_route(1, 32, 8, 128, 131072, 256, True).kind == "chunks"
+    assert choose_route(1, 32, 8, 64, 8192, 256, True).kind == "chunks"
+    # Two kv heads of 1024 tokens: the split single pass, 23.2 us (17.9 at
+    # head_dim 64) vs key chunks 29.6 (26.7).
+    for D in (128, 64):
+        assert choose_route(1, 8, 2, 1024, 1024, 256, True, D).kind == "single"
+
+
 def test_fwd_split_launch_validation(lib):
     f = lib.gqa_fwd_split_launch
     args = lambda lse, ws, cnt, ns: (_FAKE, _S4, _FAKE, _S4, _FAKE, _S4, _FAKE, _S4, lse, ws, cnt, ns,
