@@ -26,7 +26,8 @@ using gqa::TensorRef;
 // scheduling counters (also for n_split = 0); gqa_fwd_split_launch with
 // counters schedules the work items across the XCDs dynamically.
 // 11: gqa_fwd_chunks_launch (single pass over key chunks + split combine).
-constexpr int kAbiVersion = 11;
+// 12: gqa_paged_fwd_chunks_launch (the same over a paged cache).
+constexpr int kAbiVersion = 12;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -163,6 +164,13 @@ int check_lse(const float* lse) {
   if (lse == nullptr) return GQA_E_NULL;
   return (reinterpret_cast<uintptr_t>(lse) & 3u) != 0 ? GQA_E_STRIDE : GQA_OK;
 }
+
+int paged_fwd_impl(const void* q, const int64_t q_stride[4], const void* k_cache,
+                   const int64_t k_cache_stride[4], const void* v_cache, const int64_t v_cache_stride[4],
+                   const int* block_table, int table_stride, const int* seq_lens, const int* q_start,
+                   const int* q_len, int block_size, int max_seq_len, void* o, const int64_t o_stride[4],
+                   float* lse, float* workspace, int kv_splits, int batch, int num_heads, int num_kv_heads,
+                   int seq_q, int head_dim, float scale_log2, int causal, int dtype, void* stream);
 
 }  // namespace
 
@@ -304,45 +312,22 @@ int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4], const void* k
                          float* lse, int batch,
                          int num_heads, int num_kv_heads, int seq_q, int head_dim, float scale_log2, int causal,
                          int dtype, void* stream) {
-  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
-  if (rc) return rc;
-  const int G = num_heads / num_kv_heads;
-  if (G > gqa::kFwdRows) return GQA_E_GROUP;
-  // Each LDS-DMA instruction loads 512 / head_dim rows, which must lie in
-  // one block.
-  if (block_size < 512 / head_dim || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
-    return GQA_E_BLOCK;
-  if (table_stride < 0 || (int64_t)table_stride * block_size < (int64_t)max_seq_len) return GQA_E_BLOCK;
-  if (batch == 0 || seq_q == 0) return GQA_OK;
-  if (seq_lens == nullptr) return GQA_E_NULL;
-  if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0) return GQA_E_STRIDE;
-  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
-  if ((rc = check_varlen(q_start, q_len))) return rc;
-  if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
-  if (max_seq_len > 0) {
-    if (block_table == nullptr) return GQA_E_NULL;
-    if ((reinterpret_cast<uintptr_t>(block_table) & 3u) != 0) return GQA_E_STRIDE;
-    if ((rc = check_tensor(k_cache, k_cache_stride)) || (rc = check_tensor(v_cache, v_cache_stride))) return rc;
-  }
+  return paged_fwd_impl(q, q_stride, k_cache, k_cache_stride, v_cache, v_cache_stride, block_table, table_stride,
+                        seq_lens, q_start, q_len, block_size, max_seq_len, o, o_stride, lse, nullptr, 0, batch,
+                        num_heads, num_kv_heads, seq_q, head_dim, scale_log2, causal, dtype, stream);
+}
 
-  gqa::FwdParams p{};
-  p.q = ref(q, q_stride);
-  p.k = cache_ref(k_cache, k_cache_stride);
-  p.v = cache_ref(v_cache, v_cache_stride);
-  p.o = ref(o, o_stride);
-  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, G, scale_log2, causal ? 1 : 0};
-  p.block_m = gqa::kFwdRows / G;
-  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
-  p.lse = lse;
-  p.block_table = block_table;
-  p.seq_lens = seq_lens;
-  p.table_stride = table_stride;
-  int shift = 0;
-  while ((1 << shift) < block_size) ++shift;
-  p.block_shift = shift;
-  p.q_start = q_start;
-  p.q_len = q_len;
-  return to_code(gqa::launch_paged_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+int gqa_paged_fwd_chunks_launch(const void* q, const int64_t q_stride[4], const void* k_cache,
+                                const int64_t k_cache_stride[4], const void* v_cache,
+                                const int64_t v_cache_stride[4], const int* block_table, int table_stride,
+                                const int* seq_lens, const int* q_start, const int* q_len, int block_size,
+                                int max_seq_len, void* o, const int64_t o_stride[4], float* lse, float* workspace,
+                                int kv_splits, int batch, int num_heads, int num_kv_heads, int seq_q, int head_dim,
+                                float scale_log2, int causal, int dtype, void* stream) {
+  if (kv_splits < 1 || kv_splits > GQA_MAX_SPLITS) return GQA_E_SPLITS;
+  return paged_fwd_impl(q, q_stride, k_cache, k_cache_stride, v_cache, v_cache_stride, block_table, table_stride,
+                        seq_lens, q_start, q_len, block_size, max_seq_len, o, o_stride, lse, workspace, kv_splits,
+                        batch, num_heads, num_kv_heads, seq_q, head_dim, scale_log2, causal, dtype, stream);
 }
 
 int gqa_paged_cache_write_launch(const void* k, const int64_t k_stride[3], const void* v,
@@ -577,6 +562,74 @@ int reduce_impl(const float* workspace, int splits, void* o, const int64_t o_str
   p.q_start = q_start;
   p.q_len = q_len;
   return to_code(gqa::launch_split_reduce(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+// The paged single pass (gqa_paged_fwd_launch) and, with kv_splits > 0, the
+// same over key chunks into `workspace` followed by the split combine
+// (gqa_paged_fwd_chunks_launch).
+int paged_fwd_impl(const void* q, const int64_t q_stride[4], const void* k_cache,
+                   const int64_t k_cache_stride[4], const void* v_cache, const int64_t v_cache_stride[4],
+                   const int* block_table, int table_stride, const int* seq_lens, const int* q_start,
+                   const int* q_len, int block_size, int max_seq_len, void* o, const int64_t o_stride[4],
+                   float* lse, float* workspace, int kv_splits, int batch, int num_heads, int num_kv_heads,
+                   int seq_q, int head_dim, float scale_log2, int causal, int dtype, void* stream) {
+  int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
+  if (rc) return rc;
+  const int G = num_heads / num_kv_heads;
+  if (G > gqa::kFwdRows) return GQA_E_GROUP;
+  // Each LDS-DMA instruction loads 512 / head_dim rows, which must lie in
+  // one block.
+  if (block_size < 512 / head_dim || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
+    return GQA_E_BLOCK;
+  if (table_stride < 0 || (int64_t)table_stride * block_size < (int64_t)max_seq_len) return GQA_E_BLOCK;
+  if (batch == 0 || seq_q == 0) return GQA_OK;
+  if (seq_lens == nullptr) return GQA_E_NULL;
+  if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0) return GQA_E_STRIDE;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  if (kv_splits > 0 && workspace == nullptr) return GQA_E_NULL;
+  if (kv_splits > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return GQA_E_STRIDE;
+  if ((rc = check_varlen(q_start, q_len))) return rc;
+  if ((rc = check_tensor(q, q_stride)) || (rc = check_tensor(o, o_stride))) return rc;
+  if (max_seq_len > 0) {
+    if (block_table == nullptr) return GQA_E_NULL;
+    if ((reinterpret_cast<uintptr_t>(block_table) & 3u) != 0) return GQA_E_STRIDE;
+    if ((rc = check_tensor(k_cache, k_cache_stride)) || (rc = check_tensor(v_cache, v_cache_stride))) return rc;
+  }
+
+  gqa::FwdParams p{};
+  p.q = ref(q, q_stride);
+  p.k = cache_ref(k_cache, k_cache_stride);
+  p.v = cache_ref(v_cache, v_cache_stride);
+  p.o = ref(o, o_stride);
+  p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, G, scale_log2, causal ? 1 : 0};
+  p.block_m = gqa::kFwdRows / G;
+  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  p.lse = lse;
+  p.block_table = block_table;
+  p.seq_lens = seq_lens;
+  p.table_stride = table_stride;
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  p.block_shift = shift;
+  p.q_start = q_start;
+  p.q_len = q_len;
+  if (kv_splits == 0) return to_code(gqa::launch_paged_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+  // Key chunks: chunk c of every query block covers key tiles [c * ct,
+  // (c + 1) * ct) of the longest sequence's range; the partials go to the
+  // split-KV workspace layout and the split combine writes o (and lse),
+  // token-major with variable query lengths.
+  p.lse = nullptr;
+  const int tiles = (max_seq_len + gqa::kFwdTileKeys - 1) / gqa::kFwdTileKeys;
+  p.kv_splits = kv_splits;
+  p.kv_chunk_tiles = std::max((tiles + kv_splits - 1) / kv_splits, 1);
+  const size_t rows = (size_t)batch * num_heads * seq_q * kv_splits;
+  p.ws_acc = workspace;
+  p.ws_m = workspace + rows * head_dim;
+  p.ws_l = p.ws_m + rows;
+  rc = to_code(gqa::launch_paged_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+  if (rc) return rc;
+  return reduce_impl(workspace, kv_splits, o, o_stride, lse, batch, num_heads, seq_q, head_dim, dtype, stream,
+                     q_start, q_len);
 }
 
 // ---------------------------------------------------------------------------

@@ -147,8 +147,8 @@ __device__ __forceinline__ void mphase_pipe() {
 // next item's first K/V tiles and Q, and the output stores drain while
 // those loads are in flight.  The workgroup launch between items leaves the
 // critical path.
-// KC: key chunks (FwdParams::kv_splits > 0; contiguous K/V only), a
-// separate instance so the others keep their registers.
+// KC: key chunks (FwdParams::kv_splits > 0), a separate instance so the
+// others keep their registers.
 template <int DT, int D, int PG, bool KC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void gqa_fwd_kernel(
     FwdParams p) {
@@ -195,9 +195,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
   // split, the n_split heaviest blocks of each (b, kv head) come as two
   // items: first the upper halves of their key ranges, then (in the usual
   // order) the lower halves and the unsplit blocks.
-  // Key chunks (contiguous K/V only): kv_splits items per query block, the
-  // blocks of one chunk consecutive (they read the same keys).
-  constexpr bool chunked = KC && PG == 0;
+  // Key chunks: kv_splits items per query block, the blocks of one chunk
+  // consecutive (they read the same keys).
+  constexpr bool chunked = KC;
   const int n_items = chunked ? p.n_mblk * p.kv_splits : p.n_mblk + p.n_split;
   const int total = n_items * dm.Hkv * dm.B;
   // The k-th item of this workgroup (-1: none).  One item per workgroup
@@ -926,7 +926,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4
 
 template <int DT, int D, int PG>
 static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
-  const int per_bh = (PG == 0 && p.kv_splits > 0) ? p.n_mblk * p.kv_splits : p.n_mblk + p.n_split;
+  const int per_bh = p.kv_splits > 0 ? p.n_mblk * p.kv_splits : p.n_mblk + p.n_split;
   const int total = per_bh * p.dm.Hkv * p.dm.B;
   if (total <= 0) return hipSuccess;
   int grid = total;
@@ -943,8 +943,8 @@ static hipError_t launch_fwd_t(FwdParams p, hipStream_t stream) {
   } else {
     p.sched = nullptr;
   }
-  if (PG == 0 && p.kv_splits > 0)
-    hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, 0, true>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
+  if (p.kv_splits > 0)
+    hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG, true>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
   else
     hipLaunchKernelGGL((gqa_fwd_kernel<DT, D, PG>), dim3(grid), dim3(kFwdThreads), 0, stream, p);
   return hipGetLastError();

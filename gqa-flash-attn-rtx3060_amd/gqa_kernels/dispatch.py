@@ -182,16 +182,20 @@ def _list_makespan(items, cu_count: int, persistent: bool = False) -> float:
 
 
 def chunks_makespan(tiles, kv_splits: int, n_bh: int, cu_count: int, rows: int, head_dim: int,
-                    causal: bool = True) -> float:
+                    causal: bool = True, persistent: bool = None) -> float:
     """Modelled run time (tile steps) of the single pass over key chunks:
     items (b, kv head) x chunk x query block (heavy first under causal),
     chunk c covering tiles [c * ct, (c + 1) * ct) of its block's range, plus
-    the combine (launch and its read of rows x kv_splits partials)."""
+    the combine (launch and its read of rows x kv_splits partials).
+    `persistent` (default: head_dim 128): the persistent kernel over
+    contiguous K/V; paged caches run one workgroup per item."""
     n = len(tiles)
     ct = max(1, -(-max(tiles) // kv_splits))
     order = list(range(n - 1, -1, -1)) if causal else list(range(n))
     per_bh = [min(ct, max(tiles[m] - c * ct, 0)) + CHUNK_ITEM_OVERHEAD for c in range(kv_splits) for m in order]
-    first = _list_makespan(per_bh * n_bh, cu_count, persistent=head_dim == 128)
+    if persistent is None:
+        persistent = head_dim == 128
+    first = _list_makespan(per_bh * n_bh, cu_count, persistent)
     # The fp32 partials are written by the first pass and read back by the
     # combine launch, each at about COMBINE_BYTES_PER_US.
     combine_us = COMBINE_LAUNCH_US + CHUNK_PARTIAL_PASSES * rows * kv_splits * (head_dim + 2) * 4 / COMBINE_BYTES_PER_US
@@ -199,7 +203,8 @@ def chunks_makespan(tiles, kv_splits: int, n_bh: int, cu_count: int, rows: int, 
 
 
 def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
-                     cu_count: int, causal: bool, head_dim: int = 128, base: float = None) -> int:
+                     cu_count: int, causal: bool, head_dim: int = 128, base: float = None,
+                     persistent: bool = None) -> int:
     """Key chunks per query block for the single pass (0: none).
 
     With fewer query blocks than compute units (chunked prefill or a long
@@ -207,7 +212,8 @@ def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
     block's key range into kv_splits chunks (a power of two, each at least
     CHUNK_MIN_TILES tiles) fills them, at the cost of the fp32 partials and
     the combine launch.  Taken when the model beats the single pass (`base`:
-    its modelled time) by FWD_SPLIT_GAIN."""
+    its modelled time) by FWD_SPLIT_GAIN.  `persistent` as chunks_makespan
+    (False for paged caches)."""
     group = num_heads // num_kv_heads
     block_m = max(1, FWD_ROWS // group)
     n_mblk = _cdiv(seq_q, block_m)
@@ -215,13 +221,15 @@ def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
     if n_mblk * n_bh >= cu_count or seq_q == 0:
         return 0
     tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, seq_kv, causal)
+    if persistent is None:
+        persistent = head_dim == 128
     if base is None:
-        base = fwd_split_makespan(tiles, 0, n_bh, cu_count, causal, persistent=head_dim == 128)
+        base = fwd_split_makespan(tiles, 0, n_bh, cu_count, causal, persistent=persistent)
     rows = batch * num_heads * seq_q
     best, best_s = base, 0
     s = 2
     while s <= _lib.GQA_MAX_SPLITS and -(-max(tiles) // s) >= CHUNK_MIN_TILES:
-        t = chunks_makespan(tiles, s, n_bh, cu_count, rows, head_dim, causal)
+        t = chunks_makespan(tiles, s, n_bh, cu_count, rows, head_dim, causal, persistent)
         if t < best:
             best, best_s = t, s
         s *= 2

@@ -39,6 +39,7 @@ from typing import Dict, Hashable, List, Optional, Sequence
 import torch
 
 from . import _lib
+from .dispatch import SPLIT_MIN_KV, choose_kv_chunks
 from .gqa_split import _workspace_buffer, stream_handle, workspace_bytes
 
 __all__ = [
@@ -46,6 +47,7 @@ __all__ = [
     "write_kv",
     "paged_chunk",
     "paged_splits",
+    "paged_kv_chunks",
     "PagedKVCache",
     "PagedAttentionMetadata",
     "GQAPagedAttention",
@@ -185,6 +187,24 @@ def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int, 
     return "single"
 
 
+def paged_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
+                    cu_count: int, causal: bool = True, head_dim: int = 128) -> int:
+    """Key chunks per query block for the paged single pass (0: none).
+
+    The paged single pass runs one workgroup per query block; with fewer
+    blocks than compute units against long sequences (a chunk of new tokens
+    over a long cached prefix, few sequences) most CUs idle, and splitting
+    every block's key range (gqa_paged_fwd_chunks_launch) fills them, at the
+    cost of the fp32 partials and the combine launch: the count of
+    dispatch.choose_kv_chunks for a kernel of one workgroup per item, from
+    SPLIT_MIN_KV keys on (the length from which the reference splits the key
+    axis at all)."""
+    if max_seq_len < SPLIT_MIN_KV:
+        return 0
+    return choose_kv_chunks(batch, num_heads, num_kv_heads, seq_q, max_seq_len, cu_count, causal, head_dim,
+                            persistent=False)
+
+
 def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
                     max_seq_len: Optional[int] = None, scale: Optional[float] = None,
                     splits: Optional[int] = None, return_lse: bool = False,
@@ -215,8 +235,10 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             (batch, num_heads, seq_q).
         out: optional (batch, num_heads, seq_q, head_dim) tensor of q's dtype
             (any strides with 16-byte aligned rows) to write o into.
-        route: "split" or "single" to force a kernel (default: paged_route;
-            "single" needs block_size >= 512 / head_dim).
+        route: "split", "single" or "chunks" to force a kernel (default:
+            paged_route, and "chunks" in place of "single" when
+            paged_kv_chunks finds few query blocks against long sequences;
+            "single" and "chunks" need block_size >= 512 / head_dim).
         query_start, query_lens, max_query_len: variable query lengths.  q
             is then token-major (num_tokens, num_heads, head_dim); sequence
             b's queries are tokens query_start[b] .. + query_lens[b] - 1
@@ -287,10 +309,29 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
     stream = stream_handle(q.device)
-    route = route or paged_route(num_heads, num_kv_heads, seq_q, block_size, head_dim)
-    assert route in ("split", "single") and (route == "split" or block_size >= single_pass_min_block(head_dim))
+    kv_chunks = 0
+    if route is None:
+        route = paged_route(num_heads, num_kv_heads, seq_q, block_size, head_dim)
+        if route == "single":
+            kv_chunks = paged_kv_chunks(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev),
+                                        causal, head_dim)
+            route = "chunks" if kv_chunks else route
+    elif route == "chunks":
+        kv_chunks = splits if splits is not None else max(2, paged_kv_chunks(
+            batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), causal, head_dim))
+    assert route in ("split", "single", "chunks")
+    assert route == "split" or block_size >= single_pass_min_block(head_dim)
     lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if return_lse else None
     lse_p = None if lse is None else lse.data_ptr()
+    if route == "chunks":
+        workspace = _workspace_buffer(q.device, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, kv_chunks))
+        _lib.check(lib.gqa_paged_fwd_chunks_launch(
+            q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),
+            v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
+            seq_lens.data_ptr(), qs_p, ql_p, block_size, max_seq_len, out.data_ptr(), ost,
+            lse_p, workspace.data_ptr(), kv_chunks, batch, num_heads, num_kv_heads, seq_q, head_dim,
+            scale * LOG2E, int(bool(causal)), dtype, stream))
+        return out if lse is None else (out, lse)
     if route == "single":
         _lib.check(lib.gqa_paged_fwd_launch(
             q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),

@@ -340,6 +340,30 @@ int gqa_paged_fwd_launch(const void* q, const int64_t q_stride[4],
                          int seq_q, int head_dim,
                          float scale_log2, int causal, int dtype, void* stream);
 
+/* gqa_paged_fwd_launch over key chunks, for few query blocks against long
+ * sequences (a chunk of new tokens appended to a long cached prefix, with
+ * few sequences in the batch): every query block runs as kv_splits work
+ * items, item c over key tiles [c * ct, (c + 1) * ct) with ct =
+ * ceil(ceil(max_seq_len / 64) / kv_splits), each storing its rows' fp32
+ * partials in `workspace` (gqa_split_workspace_bytes(batch, num_heads,
+ * seq_q, head_dim, kv_splits) bytes, 16-byte aligned), and the split combine
+ * then writes o (and lse, which may be NULL), token-major with variable
+ * query lengths.  Arguments otherwise as gqa_paged_fwd_launch; kv_splits in
+ * [1, GQA_MAX_SPLITS].  No counterpart in the reference (whose roadmap,
+ * README.md:140-146, has the paged cache); the contiguous form is
+ * gqa_fwd_chunks_launch. */
+int gqa_paged_fwd_chunks_launch(const void* q, const int64_t q_stride[4],
+                                const void* k_cache, const int64_t k_cache_stride[4],
+                                const void* v_cache, const int64_t v_cache_stride[4],
+                                const int* block_table, int table_stride,
+                                const int* seq_lens, const int* q_start, const int* q_len,
+                                int block_size, int max_seq_len,
+                                void* o, const int64_t o_stride[4], float* lse,
+                                float* workspace, int kv_splits,
+                                int batch, int num_heads, int num_kv_heads,
+                                int seq_q, int head_dim,
+                                float scale_log2, int causal, int dtype, void* stream);
+
 /* gqa_split_reduce_launch for variable query lengths (q_start, q_len as
  * above, non-NULL; o token-major); lse may be NULL or receives (tokens,
  * num_heads). */

@@ -124,11 +124,13 @@ def test_paged_single_pass_matches_oracle(B, Hq, Hkv, Sq, lens, D, bs, dtype, ca
     if hnd:
         kd, vd = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (kc, vc))
     args = (q.to(DEV), kd, vd, table.to(DEV), seq_lens.to(DEV), causal)
-    o, lse = paged_attention(*args, max_seq_len=max(lens), return_lse=True)
+    o, lse = paged_attention(*args, max_seq_len=max(lens), return_lse=True, route="single")
     o_split = paged_attention(*args, max_seq_len=max(lens), route="split")
+    o_default = paged_attention(*args, max_seq_len=max(lens))  # single, or key chunks (paged_kv_chunks)
     torch.cuda.synchronize()
     _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype)
     _check(o_split, None, q, kc, vc, table, seq_lens, causal, dtype)
+    _check(o_default, None, q, kc, vc, table, seq_lens, causal, dtype)
 
 
 @pytest.mark.parametrize("pad", [32, 16])
