@@ -185,6 +185,30 @@ def test_paged_fwd_empty_is_noop(lib):
     assert _pfwd(lib, Sq=0, q=None, k=None, v=None, table=None, lens=None, o=None) == 0
 
 
+def _pchunks(lib, ws=_FAKE, splits=8, **kw):
+    a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16, lens=_FAKE,
+             qstart=None, qlen=None, bs=64, max_len=1024, o=_FAKE, os=_S4, lse=None, B=2, Hq=32, Hkv=8, Sq=128,
+             D=128, scale=0.1275, causal=1, dtype=0)
+    a.update(kw)
+    return lib.gqa_paged_fwd_chunks_launch(a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"],
+                                           a["tstride"], a["lens"], a["qstart"], a["qlen"], a["bs"], a["max_len"],
+                                           a["o"], a["os"], a["lse"], ws, splits, a["B"], a["Hq"], a["Hkv"],
+                                           a["Sq"], a["D"], a["scale"], a["causal"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(splits=0), -5), (dict(splits=1025), -5),                   # kv_splits in [1, GQA_MAX_SPLITS]
+    (dict(ws=None), -7), (dict(ws=ctypes.c_void_p((1 << 20) + 8)), -4),  # workspace: non-NULL, 16-byte aligned
+    (dict(bs=2), -8), (dict(lens=None), -7), (dict(D=96), -2),       # as gqa_paged_fwd_launch
+])
+def test_paged_chunks_validation(lib, kw, code):
+    assert _pchunks(lib, **kw) == code
+
+
+def test_paged_chunks_empty_is_noop(lib):
+    assert _pchunks(lib, B=0, q=None, k=None, v=None, table=None, lens=None, o=None, ws=None) == 0
+
+
 def test_reduce_varlen_validation(lib):
     r = lib.gqa_split_reduce_varlen_launch
     assert r(_FAKE, 8, _FAKE, _S4, None, None, None, 2, 32, 16, 128, 0, None) == -7
