@@ -6,7 +6,8 @@ TFLOP/s at the Llama-3.1-8B GQA shape, seq 16384 (B=1, Hq=32, Hkv=8, D=128,
 bf16); the ``decode`` object carries split-KV decode at seq_kv 131072
 (microseconds and HBM GB/s), ``paged_decode`` the same decode over a paged
 KV cache (gqa_kernels.paged) at two block sizes / in-block layouts,
-``paged_prefill`` the chunked-prefill shape over a paged cache, and
+``paged_prefill`` the chunked-prefill shape over a paged cache (and a
+128-token chunk over a 16384-key paged prefix), and
 ``configs`` every BASELINE config (prefill 2048-16384, decode 2048-131072,
 chunked prefill, the 70B decode shape) with its time and the fraction of the
 roofline (MFMA or HBM) that bounds it, ``extras`` the same for a 16-token
@@ -477,15 +478,24 @@ def paged_prefill(torch, steps, warmup):
     """The chunked-prefill BASELINE shape (B=4, 512 new tokens attending 8192
     keys, causal) over a paged cache (gqa_kernels.paged, single-pass route),
     128-key HND blocks, 64-key NHD blocks and 16-key NHD blocks (vLLM's
-    default block size) in random order."""
+    default block size) in random order; then one sequence's 128-token
+    chunk over a 16384-key prefix in 16-key NHD blocks (the key-chunk
+    route)."""
     from gqa_kernels.paged import paged_attention
-    b, sq, skv = 4, 512, 8192
+    out = []
+    for b, sq, skv, legs in ((4, 512, 8192, ((128, "HND"), (64, "NHD"), (16, "NHD"))),
+                             (1, 128, 16384, ((16, "NHD"),))):
+        out += _paged_prefill_legs(torch, paged_attention, b, sq, skv, legs, steps, warmup)
+    return out
+
+
+def _paged_prefill_legs(torch, paged_attention, b, sq, skv, legs, steps, warmup):
     g = torch.Generator(device="cuda").manual_seed(4)
     q = torch.randn(b, HQ, sq, D, device="cuda", generator=g).to(torch.bfloat16)
     lens = torch.full((b,), skv, dtype=torch.int32, device="cuda")
     fl = flops(b, HQ, sq, skv, D)
     out = []
-    for bs, layout in ((128, "HND"), (64, "NHD"), (16, "NHD")):
+    for bs, layout in legs:
         nblk = b * skv // bs
         shape = (nblk, HKV, bs, D) if layout == "HND" else (nblk, bs, HKV, D)
         kc, vc = (torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16) for _ in range(2))

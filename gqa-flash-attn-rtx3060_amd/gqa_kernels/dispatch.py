@@ -8,8 +8,8 @@ HIP kernels through the C ABI of libgqa_hip.so.
 """
 from __future__ import annotations
 
+import bisect
 import functools
-import heapq
 import math
 from dataclasses import dataclass
 
@@ -142,42 +142,99 @@ def fwd_split_makespan(tiles, n_split: int, n_bh: int, cu_count: int, causal: bo
     items = [tiles[n - 1 - i] - tiles[n - 1 - i] // 2 + mo for i in range(n_split)]
     for pid in order:
         items.append(tiles[pid] // 2 + mo if pid >= n - n_split else tiles[pid])
-    return _list_makespan([c + FWD_ITEM_OVERHEAD for c in items] * n_bh, cu_count, persistent)
+    runs = []
+    for c in items:
+        _push_run(runs, c + FWD_ITEM_OVERHEAD, 1)
+    return _list_makespan(runs, n_bh, cu_count, persistent)
 
 
-def _list_makespan(items, cu_count: int, persistent: bool = False) -> float:
-    """Run time (tile steps) of `items` (costs in the kernel's item order):
-    each XCD (cu_count / 8 CUs) takes its contiguous share.  The persistent
-    kernel with fewer than FWD_DYN_MIN_ITEMS_PER_WG items per workgroup
-    deals fixed lists: workgroup `slot` of XCD x takes items slot, 2 S - 1 -
-    slot, 2 S + slot, ... of the XCD's share (S workgroups on the XCD:
-    gqa_fwd.hip item_at).  Otherwise (the dynamic schedule, or one
-    workgroup per item) each CU takes the next item when free."""
-    total = len(items)
+def _push_run(runs, cost, count: int) -> None:
+    if count <= 0:
+        return
+    if runs and runs[-1][0] == cost:
+        runs[-1][1] += count
+    else:
+        runs.append([cost, count])
+
+
+def _slice_runs(runs, period: int, lo: int, cnt: int):
+    """Runs of items [lo, lo + cnt) of `runs` (one period) repeated end to end."""
+    out, i, off = [], 0, lo % period
+    while off >= runs[i][1]:
+        off -= runs[i][1]
+        i += 1
+    while cnt > 0:
+        take = min(runs[i][1] - off, cnt)
+        _push_run(out, runs[i][0], take)
+        cnt -= take
+        off, i = 0, (i + 1) % len(runs)
+    return out
+
+
+def _greedy_runs(runs, n: int) -> float:
+    """Makespan of n CUs each taking the next item when free (the least
+    loaded CU takes it), items in order.  A run of items of one cost c on
+    loads within c of each other is dealt round-robin in load order (each
+    item lands on the least loaded CU and leaves it the most loaded), so it
+    is applied as whole rounds plus the remainder on the least loaded CUs."""
+    loads = [0.0] * n  # ascending
+    for c, k in runs:
+        while k:
+            if loads[-1] - loads[0] <= c:
+                full, rem = divmod(k, n)
+                if full:
+                    loads = [x + full * c for x in loads]
+                if rem:
+                    loads = loads[rem:] + [x + c for x in loads[:rem]]
+                break
+            bisect.insort(loads, loads.pop(0) + c)
+            k -= 1
+    return loads[-1]
+
+
+def _list_makespan(runs, n_rep: int, cu_count: int, persistent: bool = False) -> float:
+    """Run time (tile steps) of the items of one (b, kv head), given as runs
+    [cost, count] in the kernel's item order, repeated for n_rep (b, kv head)
+    pairs: each XCD (cu_count / 8 CUs) takes its contiguous share of the
+    whole list.  The persistent kernel with fewer than
+    FWD_DYN_MIN_ITEMS_PER_WG items per workgroup deals fixed lists:
+    workgroup `slot` of XCD x takes items slot, 2 S - 1 - slot, 2 S + slot,
+    ... of the XCD's share (S workgroups on the XCD: gqa_fwd.hip item_at).
+    Otherwise (the dynamic schedule, or one workgroup per item) each CU
+    takes the next item when free.  XCD shares with the same start within
+    the period and the same length are scheduled once (with 8 kv heads
+    every XCD's share is the same list)."""
+    period = sum(k for _, k in runs)
+    total = period * n_rep
+    if total == 0:
+        return 0.0
     n_wg = min(total, cu_count)
     q, r = divmod(total, 8)
-    worst = 0.0
-    if persistent and total < FWD_DYN_MIN_ITEMS_PER_WG * n_wg:
-        for x in range(8):
-            lo, cnt = x * q + min(x, r), q + (1 if x < r else 0)
-            slots = (n_wg - x + 7) >> 3
-            for slot in range(slots):
-                t, j = 0.0, 0
-                while True:
-                    e = j * slots + (slots - 1 - slot if j & 1 else slot)
-                    if e >= cnt:
-                        break
-                    t += items[lo + e]
-                    j += 1
-                worst = max(worst, t)
-        return worst
+    static = persistent and total < FWD_DYN_MIN_ITEMS_PER_WG * n_wg
+    flat = [c for c, k in runs for _ in range(k)] if static else None
     per_xcd = max(1, cu_count // 8)
+    seen = {}
+    worst = 0.0
     for x in range(8):
-        lo = x * q + min(x, r)
-        heap = [0.0] * per_xcd
-        for w in range(lo, lo + q + (1 if x < r else 0)):
-            heapq.heapreplace(heap, heap[0] + items[w])
-        worst = max(worst, max(heap))
+        lo, cnt = x * q + min(x, r), q + (1 if x < r else 0)
+        slots = (n_wg - x + 7) >> 3
+        key = (lo % period, cnt, slots if static else 0)
+        if key in seen or cnt == 0:
+            continue
+        if static:
+            # Rows of `slots` items, odd rows reversed (right-aligned when
+            # short): workgroup `slot` sums column `slot`.
+            share = (flat * (-(-(lo % period + cnt) // period)))[lo % period:lo % period + cnt]
+            rows = []
+            for j, i in enumerate(range(0, cnt, slots)):
+                row = share[i:i + slots]
+                pad = [0] * (slots - len(row))
+                rows.append(pad + row[::-1] if j & 1 else row + pad)
+            t_x = float(max(map(sum, zip(*rows))))
+        else:
+            t_x = _greedy_runs(_slice_runs(runs, period, lo, cnt), per_xcd)
+        seen[key] = t_x
+        worst = max(worst, t_x)
     return worst
 
 
@@ -192,10 +249,19 @@ def chunks_makespan(tiles, kv_splits: int, n_bh: int, cu_count: int, rows: int, 
     n = len(tiles)
     ct = max(1, -(-max(tiles) // kv_splits))
     order = list(range(n - 1, -1, -1)) if causal else list(range(n))
-    per_bh = [min(ct, max(tiles[m] - c * ct, 0)) + CHUNK_ITEM_OVERHEAD for c in range(kv_splits) for m in order]
+    # Chunks below every block's end are full (ct tiles), chunks past every
+    # block's end are empty; only the ones between differ per block.
+    n_full = min(kv_splits, min(tiles) // ct)
+    n_busy = min(kv_splits, -(-max(tiles) // ct))
+    runs = []
+    _push_run(runs, ct + CHUNK_ITEM_OVERHEAD, n_full * n)
+    for c in range(n_full, n_busy):
+        for m in order:
+            _push_run(runs, min(ct, max(tiles[m] - c * ct, 0)) + CHUNK_ITEM_OVERHEAD, 1)
+    _push_run(runs, CHUNK_ITEM_OVERHEAD, (kv_splits - n_busy) * n)
     if persistent is None:
         persistent = head_dim == 128
-    first = _list_makespan(per_bh * n_bh, cu_count, persistent)
+    first = _list_makespan(runs, n_bh, cu_count, persistent)
     # The fp32 partials are written by the first pass and read back by the
     # combine launch, each at about COMBINE_BYTES_PER_US.
     combine_us = COMBINE_LAUNCH_US + CHUNK_PARTIAL_PASSES * rows * kv_splits * (head_dim + 2) * 4 / COMBINE_BYTES_PER_US

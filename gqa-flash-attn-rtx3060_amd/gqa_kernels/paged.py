@@ -31,6 +31,7 @@ of block ``block_table[b, j // block_size]``.  A slot index is
 """
 from __future__ import annotations
 
+import functools
 import math
 import threading
 from dataclasses import dataclass
@@ -187,6 +188,7 @@ def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int, 
     return "single"
 
 
+@functools.lru_cache(maxsize=4096)
 def paged_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
                     cu_count: int, causal: bool = True, head_dim: int = 128) -> int:
     """Key chunks per query block for the paged single pass (0: none).
@@ -198,7 +200,8 @@ def paged_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, m
     cost of the fp32 partials and the combine launch: the count of
     dispatch.choose_kv_chunks for a kernel of one workgroup per item, from
     SPLIT_MIN_KV keys on (the length from which the reference splits the key
-    axis at all)."""
+    axis at all).  Cached: every layer of a model step asks with the same
+    arguments."""
     if max_seq_len < SPLIT_MIN_KV:
         return 0
     return choose_kv_chunks(batch, num_heads, num_kv_heads, seq_q, max_seq_len, cu_count, causal, head_dim,

@@ -380,6 +380,44 @@ def test_fwd_split_static_schedule_model():
         assert fwd_split_makespan(tiles, ns, n_bh, cu) == worst
 
 
+def test_chunks_greedy_schedule_model():
+    """The key-chunk model for one workgroup per item (paged caches) or the
+    dynamic schedule: items per (b, kv head) chunk-major, blocks heavy-first
+    within a chunk, each of min(ct, tiles left) + CHUNK_ITEM_OVERHEAD steps;
+    each XCD's CUs take its contiguous share of the whole list, the next
+    item going to the least loaded CU.  The model schedules runs of equal
+    items in bulk; here every item is placed one at a time on a heap."""
+    import heapq
+    import random
+    from gqa_kernels.dispatch import (CHUNK_ITEM_OVERHEAD, COMBINE_BYTES_PER_US, COMBINE_LAUNCH_US,
+                                      CHUNK_PARTIAL_PASSES, TILE_STEP_US, _fwd_block_tiles, chunks_makespan)
+    rng = random.Random(9)
+    for _ in range(200):
+        block_m = rng.choice([16, 32, 64])
+        seq_q = rng.randint(1, 12 * block_m)
+        seq_kv = seq_q + rng.choice([0, rng.randint(1, 300), rng.randint(1000, 40000)])
+        causal = rng.random() < 0.7
+        tiles = _fwd_block_tiles(-(-seq_q // block_m), block_m, seq_q, seq_kv, causal)
+        ks = rng.choice([2, 4, 8, 32, 128])
+        n_bh = rng.randint(1, 20)
+        cu = rng.choice([16, 64, 256])
+        ct = max(1, -(-max(tiles) // ks))
+        order = range(len(tiles) - 1, -1, -1) if causal else range(len(tiles))
+        items = [min(ct, max(tiles[m] - c * ct, 0)) + CHUNK_ITEM_OVERHEAD for c in range(ks) for m in order] * n_bh
+        q, r = divmod(len(items), 8)
+        worst = 0
+        for x in range(8):
+            lo = x * q + min(x, r)
+            heap = [0] * max(1, cu // 8)
+            for w in range(lo, lo + q + (1 if x < r else 0)):
+                heapq.heapreplace(heap, heap[0] + items[w])
+            worst = max(worst, max(heap))
+        rows = 7 * seq_q
+        combine = COMBINE_LAUNCH_US + CHUNK_PARTIAL_PASSES * rows * ks * 130 * 4 / COMBINE_BYTES_PER_US
+        got = chunks_makespan(tiles, ks, n_bh, cu, rows, 128, causal, persistent=False)
+        assert got == pytest.approx(worst + combine / TILE_STEP_US, rel=1e-12, abs=1e-9)
+
+
 def test_fwd_split_measured_choices():
     # Causal prefill on one MI355X (us, the route taken vs the alternative):
     # G = 4, B = 2 x 1536 tokens 56.0 unsplit -> 49.3 with 6 blocks split;
