@@ -233,7 +233,9 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             keys past it are not read).  Default: the table's capacity,
             max_blocks_per_seq * block_size, which needs no device read.
         scale: score scale (default head_dim ** -0.5, the reference's).
-        splits: split count (default: ``paged_splits``).
+        splits: split count of the split route (default: ``paged_splits``),
+            or key chunks per query block of the "chunks" route (default:
+            ``paged_kv_chunks``, at least 2).
         return_lse: also return the natural-log LSE per row, fp32
             (batch, num_heads, seq_q).
         out: optional (batch, num_heads, seq_q, head_dim) tensor of q's dtype
@@ -290,6 +292,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
         max_seq_len = capacity
     assert 0 <= max_seq_len <= capacity, "max_seq_len exceeds the block table's capacity"
     dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
+    splits_given = splits is not None
     if splits is None:
         interleaved = k_cache.stride(1) != head_dim or v_cache.stride(1) != head_dim
         splits = paged_splits(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), block_size,
@@ -320,7 +323,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
                                         causal, head_dim)
             route = "chunks" if kv_chunks else route
     elif route == "chunks":
-        kv_chunks = splits if splits is not None else max(2, paged_kv_chunks(
+        kv_chunks = splits if splits_given else max(2, paged_kv_chunks(
             batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), causal, head_dim))
     assert route in ("split", "single", "chunks")
     assert route == "split" or block_size >= single_pass_min_block(head_dim)
@@ -616,22 +619,45 @@ class GQAPagedAttention(torch.nn.Module):
             paged_attention(q4, k_cache, v_cache, md.block_tables, md.seq_lens, self.causal,
                             max_seq_len=md.max_seq_len, scale=self.scale, out=o4)
             return output
-        # Mixed batch: token-major views, one launch per kernel route.
+        # Mixed batch: token-major views, one launch per kernel route over
+        # that route's sequences only (a launch spreads its sequences' work
+        # items over the XCDs in contiguous ranges, so sequences without
+        # rows in it would leave XCDs idle).  A route's sequences that are
+        # adjacent in the batch (prefills and decode steps grouped, as
+        # serving engines order them) take views of the block table and
+        # lengths; otherwise their rows are gathered on the device.  The
+        # indices, query starts and lengths of every launch go to the
+        # device in one asynchronous copy from pinned memory.
         q3, o3 = query.view(num_tokens, H, D), output.view(num_tokens, H, D)
-        starts = [0] * batch
-        for b in range(1, batch):
-            starts[b] = starts[b - 1] + md.query_lens[b - 1]
-        groups: Dict[str, List[int]] = {}
-        for b, ql in enumerate(md.query_lens):
-            if ql > 0:
-                groups.setdefault(paged_route(H, Hkv, ql, k_cache.shape[1], k_cache.shape[3]), []).append(b)
-        dev = query.device
-        for route, idx in groups.items():
-            sel = torch.tensor(idx, dtype=torch.int64).to(dev)
-            qs = torch.tensor([starts[b] for b in idx], dtype=torch.int32).to(dev)
-            ql = torch.tensor([md.query_lens[b] for b in idx], dtype=torch.int32).to(dev)
-            paged_attention(q3, k_cache, v_cache, md.block_tables.index_select(0, sel),
-                            md.seq_lens.index_select(0, sel), self.causal, max_seq_len=md.max_seq_len,
-                            scale=self.scale, out=o3, route=route, query_start=qs, query_lens=ql,
-                            max_query_len=max(md.query_lens[b] for b in idx))
+        block_size = k_cache.shape[1]
+        routes = [paged_route(H, Hkv, ql, block_size, D) if ql > 0 else None for ql in md.query_lens]
+        starts, t = [], 0
+        for ql in md.query_lens:
+            starts.append(t)
+            t += ql
+        groups = [(kind, [b for b, r in enumerate(routes) if r == kind]) for kind in ("split", "single")]
+        groups = [(kind, idx) for kind, idx in groups if idx]
+        host = []
+        for _, idx in groups:
+            host += idx + [starts[b] for b in idx] + [md.query_lens[b] for b in idx]
+        meta = torch.tensor(host, dtype=torch.int32, pin_memory=True).to(query.device, non_blocking=True)
+        max_seq_len = md.max_seq_len if md.max_seq_len is not None else md.block_tables.shape[1] * block_size
+        off = 0
+        for kind, idx in groups:
+            n = len(idx)
+            sel, qs, ql = meta[off:off + n], meta[off + n:off + 2 * n], meta[off + 2 * n:off + 3 * n]
+            off += 3 * n
+            if idx[-1] - idx[0] + 1 == n:
+                tables, lens = md.block_tables[idx[0]:idx[-1] + 1], md.seq_lens[idx[0]:idx[-1] + 1]
+            else:
+                tables, lens = md.block_tables.index_select(0, sel), md.seq_lens.index_select(0, sel)
+            max_q = max(md.query_lens[b] for b in idx)
+            route, splits = kind, None
+            if kind == "single":
+                dev = query.device.index if query.device.index is not None else torch.cuda.current_device()
+                kc = paged_kv_chunks(n, H, Hkv, max_q, max_seq_len, _cu_count(dev), self.causal, D)
+                route, splits = ("chunks", kc) if kc else ("single", None)
+            paged_attention(q3, k_cache, v_cache, tables, lens, self.causal, max_seq_len=max_seq_len,
+                            scale=self.scale, out=o3, route=route, splits=splits, query_start=qs,
+                            query_lens=ql, max_query_len=max_q)
         return output

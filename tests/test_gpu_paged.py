@@ -408,26 +408,37 @@ def test_paged_variable_query_lengths(route, bs, causal):
     _check_varlen(o.cpu(), lse.cpu(), q, kc, vc, table, seq_lens, starts, qlens, causal, dt)
 
 
-@pytest.mark.parametrize("bs", [64, 16])
-def test_vllm_shaped_layer_mixed_batch(bs):
+@pytest.mark.parametrize("bs,case", [(64, "interleaved"), (16, "interleaved"), (16, "long_prefix"),
+                                     (32, "adjacent")])
+def test_vllm_shaped_layer_mixed_batch(bs, case):
     """Prefill chunks and decode steps in one call: the layer runs one launch
-    per kernel route over token-major views (16-key blocks: both routes on
-    blocks under one 64-key tile)."""
-    from gqa_kernels.paged import GQAPagedAttention, PagedAttentionMetadata, PagedKVCache
+    per kernel route over token-major views and that route's sequences —
+    views of the block table when they are adjacent in the batch, rows
+    gathered on the device otherwise (16-key blocks: both routes on blocks
+    under one 64-key tile).  With a chunk over a long prefix the prefill
+    launch takes the key chunks."""
+    from gqa_kernels.dispatch import _cu_count
+    from gqa_kernels.paged import (GQAPagedAttention, PagedAttentionMetadata, PagedKVCache, paged_kv_chunks,
+                                   paged_route)
     Hq, Hkv, D = 32, 8, 128
     dt = torch.bfloat16
     g = torch.Generator().manual_seed(17)
-    cache = PagedKVCache(300 * 64 // bs, bs, Hkv, D, dtype=dt, device=DEV)
+    long_prefix = case == "long_prefix"
+    hist_lens, qlens = {
+        "interleaved": ([1200, 0, 3000, 55], [1, 200, 1, 30]),  # decode, a whole prompt, decode, a chunk
+        "long_prefix": ([16000, 700, 0, 2], [128, 1, 0, 1]),  # a chunk, decode, an idle slot, decode
+        "adjacent": ([500, 2500, 40, 900], [64, 100, 1, 1]),  # two chunks, then two decode steps
+    }[case]
+    cache = PagedKVCache((sum(hist_lens) + sum(qlens)) // bs + 64, bs, Hkv, D, dtype=dt, device=DEV)
     layer = GQAPagedAttention(Hq, D, num_kv_heads=Hkv)
     hist = {}
-    for s, n in enumerate([1200, 0, 3000, 55]):  # sequence 1 starts empty (a fresh prompt)
+    for s, n in enumerate(hist_lens):  # a sequence of 0 keys starts empty (a fresh prompt)
         cache.add_sequence(s)
         k = torch.randn(n, Hkv, D, generator=g).to(dt)
         v = torch.randn(n, Hkv, D, generator=g).to(dt)
         if n:
             cache.append([s], k.to(DEV), v.to(DEV))
         hist[s] = (k, v)
-    qlens = [1, 200, 1, 30]  # decode, a whole prompt, decode, a chunk
     T = sum(qlens)
     query = torch.randn(T, Hq * D, generator=g).to(dt)
     key = torch.randn(T, Hkv * D, generator=g).to(dt)
@@ -435,10 +446,19 @@ def test_vllm_shaped_layer_mixed_batch(bs):
     slots = torch.tensor(sum((cache.reserve(s, n) for s, n in enumerate(qlens)), []), dtype=torch.int64)
     md = PagedAttentionMetadata(slot_mapping=slots.to(DEV), block_tables=cache.block_table(range(4)),
                                 seq_lens=cache.seq_lens(range(4)), query_lens=qlens)
+    routes = [paged_route(Hq, Hkv, n, bs) if n else None for n in qlens]
+    if case == "adjacent":
+        assert routes == ["single", "single", "split", "split"]
+    if long_prefix:
+        capacity = md.block_tables.shape[1] * bs
+        assert paged_kv_chunks(1, Hq, Hkv, 128, capacity, _cu_count(0), True, D) > 0
+    print(f"mixed batch bs={bs} hist={hist_lens} qlens={qlens}", flush=True)
     out = layer(query.to(DEV), key.to(DEV), value.to(DEV), cache.kv, md)
     torch.cuda.synchronize()
     t0 = 0
     for s, n in enumerate(qlens):
+        if n == 0:
+            continue
         k, v = hist[s]
         k = torch.cat([k, key[t0:t0 + n].view(n, Hkv, D)])
         v = torch.cat([v, value[t0:t0 + n].view(n, Hkv, D)])

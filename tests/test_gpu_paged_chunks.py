@@ -98,3 +98,23 @@ def test_paged_default_route_takes_chunks_for_long_prefixes():
     assert paged_route(32, 8, 256, 16) == "single"
     assert paged_kv_chunks(1, 32, 8, 256, 32768, 256, True, 128) > 0
     assert paged_kv_chunks(4, 32, 8, 512, 8192, 256, True, 128) == 0
+
+
+def test_paged_forced_chunks_default_count():
+    # route="chunks" without splits takes the chunk model's count (at least
+    # 2): the same result, bit for bit, as that count passed explicitly.
+    from gqa_kernels.dispatch import _cu_count
+    from gqa_kernels.paged import paged_attention, paged_kv_chunks
+    B, Hq, Hkv, Sq, D, bs = 1, 32, 8, 64, 128, 16
+    lens = [9000]
+    q, kc, vc, table, seq_lens = _paged_inputs(B, Hq, Hkv, Sq, lens, D, bs, torch.bfloat16, seed=3)
+    args = (q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), True)
+    n = max(2, paged_kv_chunks(B, Hq, Hkv, Sq, max(lens), _cu_count(0), True, D))
+    print(f"forced chunks default count {n}", flush=True)
+    o_default = paged_attention(*args, max_seq_len=max(lens), route="chunks")
+    o_explicit = paged_attention(*args, max_seq_len=max(lens), route="chunks", splits=n)
+    o_other = paged_attention(*args, max_seq_len=max(lens), route="chunks", splits=2 * n)
+    torch.cuda.synchronize()
+    assert torch.equal(o_default, o_explicit)
+    assert not torch.equal(o_default, o_other)
+    _check(o_default, None, q, kc, vc, table, seq_lens, True, torch.bfloat16)
