@@ -41,7 +41,7 @@ import torch
 
 from . import _lib
 from .dispatch import SPLIT_MIN_KV, choose_kv_chunks
-from .gqa_split import _workspace_buffer, stream_handle, workspace_bytes
+from .gqa_split import _decode_host, _workspace_buffer, stream_handle, workspace_bytes
 
 __all__ = [
     "paged_attention",
@@ -108,6 +108,7 @@ def paged_chunk(max_seq_len: int, splits: int) -> int:
     return (-(-max_seq_len // splits) + 63) & ~63
 
 
+@functools.lru_cache(maxsize=4096)
 def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
                  cu_count: int, block_size: int = 64, head_dim: int = 128,
                  heads_interleaved: bool = False) -> int:
@@ -153,10 +154,29 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
     return splits
 
 
+_ROUTE_IDS = {"split": 0, "single": 1, "chunks": 2}
+
+
+def _paged_host():
+    """The torch-tensor bindings (_gqa_host.so paged_forward / cache_write),
+    or None when they cannot be loaded: paged_attention and write_kv then
+    call the same C entry points through ctypes, with more host time per
+    call."""
+    host = _lib._host if _lib._host is not None else _decode_host()
+    return host if host is not None and hasattr(host, "paged_forward") else None
+
+
 def _rows_ready(t: torch.Tensor) -> bool:
-    """Unit last-dim stride and 16-byte aligned rows (what the kernels load)."""
-    es = t.element_size()
-    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
+    """Unit last-dim stride and 16-byte aligned rows (what the kernels load):
+    the pointer and every other stride in bytes a multiple of 16, tested at
+    once on their bitwise or."""
+    st = t.stride()
+    if st[-1] != 1:
+        return False
+    bits = 0
+    for x in st[:-1]:
+        bits |= x
+    return (t.data_ptr() | bits * t.element_size()) % 16 == 0
 
 
 def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> int:
@@ -256,6 +276,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
         o (batch, num_heads, seq_q, head_dim), or (o, lse).
     """
     varlen = query_start is not None
+    qdev = q.device
     if varlen:
         assert query_lens is not None and max_query_len is not None, "varlen needs query_lens and max_query_len"
         assert q.dim() == 3, "varlen q is (num_tokens, num_heads, head_dim)"
@@ -263,7 +284,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
         batch, seq_q = seq_lens.shape[0], int(max_query_len)
         assert query_start.dtype == torch.int32 and query_lens.dtype == torch.int32
         assert tuple(query_start.shape) == (batch,) and tuple(query_lens.shape) == (batch,)
-        assert query_start.device == q.device and query_lens.device == q.device
+        assert query_start.device == qdev and query_lens.device == qdev
         query_start, query_lens = query_start.contiguous(), query_lens.contiguous()
     else:
         batch, num_heads, seq_q, head_dim = q.shape
@@ -273,10 +294,10 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     assert head_dim in (64, 128), f"unsupported head_dim {head_dim}"
     assert k_cache.shape[3] == head_dim, "cache head_dim differs from q"
     assert q.dtype in _DTYPES and k_cache.dtype == q.dtype, "q and the caches must share one fp16/bf16 dtype"
-    assert q.is_cuda and k_cache.device == q.device
+    assert q.is_cuda and k_cache.device == qdev
     assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == batch
     assert seq_lens.dtype == torch.int32 and tuple(seq_lens.shape) == (batch,)
-    assert block_table.device == q.device and seq_lens.device == q.device
+    assert block_table.device == qdev and seq_lens.device == qdev
     if block_table.stride(1) != 1 or (batch > 1 and block_table.stride(0) < block_table.shape[1]):
         block_table = block_table.contiguous()
     seq_lens = seq_lens.contiguous()
@@ -291,7 +312,7 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     if max_seq_len is None:
         max_seq_len = capacity
     assert 0 <= max_seq_len <= capacity, "max_seq_len exceeds the block table's capacity"
-    dev = q.device.index if q.device.index is not None else torch.cuda.current_device()
+    dev = qdev.index if qdev.index is not None else torch.cuda.current_device()
     splits_given = splits is not None
     if splits is None:
         interleaved = k_cache.stride(1) != head_dim or v_cache.stride(1) != head_dim
@@ -301,20 +322,15 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
         scale = head_dim ** -0.5
 
     if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        out = torch.empty(q.shape, dtype=q.dtype, device=qdev)
     else:
-        assert tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype and out.device == q.device
+        assert tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype and out.device == qdev
         assert _rows_ready(out), "out rows must be contiguous and 16-byte aligned"
-    # Token-major q / o as the kernels address them: (unused, head, token, d).
-    qst = _lib._i64x4(0, q.stride(1), q.stride(0), 1) if varlen else _lib.strides(q)
-    ost = _lib._i64x4(0, out.stride(1), out.stride(0), 1) if varlen else _lib.strides(out)
-    qs_p = query_start.data_ptr() if varlen else None
-    ql_p = query_lens.data_ptr() if varlen else None
     lse_shape = (q.shape[0], num_heads) if varlen else (batch, num_heads, seq_q)
 
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
-    stream = stream_handle(q.device)
+    stream = stream_handle(qdev)
     kv_chunks = 0
     if route is None:
         route = paged_route(num_heads, num_kv_heads, seq_q, block_size, head_dim)
@@ -327,10 +343,23 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), causal, head_dim))
     assert route in ("split", "single", "chunks")
     assert route == "split" or block_size >= single_pass_min_block(head_dim)
-    lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if return_lse else None
+    lse = torch.empty(lse_shape, dtype=torch.float32, device=qdev) if return_lse else None
+    n_parts = kv_chunks if route == "chunks" else splits
+    workspace = None if route == "single" else _workspace_buffer(
+        qdev, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, n_parts))
+    host = _paged_host()
+    if host is not None:
+        host.paged_forward(_ROUTE_IDS[route], q, k_cache, v_cache, block_table, table_stride, seq_lens,
+                           query_start if varlen else None, query_lens if varlen else None, max_seq_len, out, lse,
+                           workspace, n_parts, batch, seq_q, scale * LOG2E, bool(causal), dtype)
+        return out if lse is None else (out, lse)
+    # Token-major q / o as the kernels address them: (unused, head, token, d).
+    qst = _lib._i64x4(0, q.stride(1), q.stride(0), 1) if varlen else _lib.strides(q)
+    ost = _lib._i64x4(0, out.stride(1), out.stride(0), 1) if varlen else _lib.strides(out)
+    qs_p = query_start.data_ptr() if varlen else None
+    ql_p = query_lens.data_ptr() if varlen else None
     lse_p = None if lse is None else lse.data_ptr()
     if route == "chunks":
-        workspace = _workspace_buffer(q.device, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, kv_chunks))
         _lib.check(lib.gqa_paged_fwd_chunks_launch(
             q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),
             v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
@@ -346,7 +375,6 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             lse_p, batch, num_heads, num_kv_heads, seq_q, head_dim,
             scale * LOG2E, int(bool(causal)), dtype, stream))
         return out if lse is None else (out, lse)
-    workspace = _workspace_buffer(q.device, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, splits))
     _lib.check(lib.gqa_paged_split_first_launch(
         q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),
         v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
@@ -382,6 +410,10 @@ def write_kv(key, value, k_cache, v_cache, slot_mapping):
     slot_mapping = slot_mapping.contiguous()
     key = key if _rows_ready(key) else key.contiguous()
     value = value if _rows_ready(value) else value.contiguous()
+    host = _paged_host()
+    if host is not None:
+        host.cache_write(key, value, k_cache, v_cache, slot_mapping, _DTYPES[key.dtype])
+        return
     lib = _lib.load()
     stream = stream_handle(key.device)
     _lib.check(lib.gqa_paged_cache_write_launch(

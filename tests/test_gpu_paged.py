@@ -468,3 +468,59 @@ def test_vllm_shaped_layer_mixed_batch(bs, case):
         got = to_np(out[t0:t0 + n].view(n, Hq, D).permute(1, 0, 2)[None])
         assert_close(got, ref_o, BASELINE_TOL[dt], f"mixed batch seq {s}")
         t0 += n
+
+
+@pytest.mark.parametrize("route,varlen", [("split", False), ("single", False), ("chunks", False),
+                                          ("split", True), ("single", True), ("chunks", True)])
+def test_paged_binding_matches_ctypes(route, varlen, monkeypatch):
+    """The torch-tensor binding (_gqa_host.so paged_forward) is what runs,
+    and it gives the same bits as the ctypes calls of the same C entry
+    points (the fallback when the binding cannot be loaded)."""
+    from gqa_kernels import paged
+    assert paged._paged_host() is not None, "the paged torch-tensor binding did not load"
+    Hq, Hkv, D, bs = 32, 8, 128, 16
+    lens = [3000, 700, 1500]
+    splits = 4 if route != "single" else None
+    if varlen:
+        qlens = [1, 37, 5] if route == "split" else [64, 37, 130]
+        q, kc, vc, table, seq_lens, starts = _varlen_inputs(Hq, Hkv, D, lens, qlens, bs, torch.bfloat16, seed=41)
+        extra = dict(query_start=torch.tensor(starts, dtype=torch.int32, device=DEV),
+                     query_lens=torch.tensor(qlens, dtype=torch.int32, device=DEV), max_query_len=max(qlens))
+    else:
+        sq = 1 if route == "split" else 64
+        q, kc, vc, table, seq_lens = _paged_inputs(3, Hq, Hkv, sq, lens, D, bs, torch.bfloat16, seed=41)
+        extra = {}
+    args = (q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), True)
+    print(f"binding vs ctypes route={route} varlen={varlen}", flush=True)
+
+    def call():
+        return paged.paged_attention(*args, max_seq_len=max(lens), return_lse=True, route=route, splits=splits,
+                                     **extra)
+
+    o1, l1 = call()
+    monkeypatch.setattr(paged, "_paged_host", lambda: None)
+    o2, l2 = call()
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_cache_write_binding_matches_ctypes(monkeypatch):
+    from gqa_kernels import paged
+    assert paged._paged_host() is not None
+    g = torch.Generator().manual_seed(2)
+    kc = torch.zeros(64, 16, 8, 128, dtype=torch.bfloat16, device=DEV)
+    key = torch.randn(40, 8, 128, generator=g).to(torch.bfloat16).to(DEV)
+    value = torch.randn(40, 8, 128, generator=g).to(torch.bfloat16).to(DEV)
+    slots = torch.randperm(64 * 16, generator=g)[:40]
+    slots[3] = -1  # padding
+    slots = slots.to(DEV)
+    k1, v1 = kc.clone(), kc.clone()
+    paged.write_kv(key, value, k1, v1, slots)
+    monkeypatch.setattr(paged, "_paged_host", lambda: None)
+    k2, v2 = kc.clone(), kc.clone()
+    paged.write_kv(key, value, k2, v2, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    keep = slots.cpu() >= 0
+    s = slots.cpu()[keep]
+    assert torch.equal(k1.view(-1, 8, 128)[s.to(DEV)], key[keep.to(DEV)])
