@@ -27,7 +27,8 @@ using gqa::TensorRef;
 // counters schedules the work items across the XCDs dynamically.
 // 11: gqa_fwd_chunks_launch (single pass over key chunks + split combine).
 // 12: gqa_paged_fwd_chunks_launch (the same over a paged cache).
-constexpr int kAbiVersion = 12;
+// 13: gqa_paged_fwd_split_launch (the paged single pass with split blocks).
+constexpr int kAbiVersion = 13;
 
 int check_dims(int B, int Hq, int Hkv, int Sq, int Skv, int D, int dtype) {
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Skv < 0) return GQA_E_SHAPE;
@@ -170,7 +171,8 @@ int paged_fwd_impl(const void* q, const int64_t q_stride[4], const void* k_cache
                    const int* block_table, int table_stride, const int* seq_lens, const int* q_start,
                    const int* q_len, int block_size, int max_seq_len, void* o, const int64_t o_stride[4],
                    float* lse, float* workspace, int kv_splits, int batch, int num_heads, int num_kv_heads,
-                   int seq_q, int head_dim, float scale_log2, int causal, int dtype, void* stream);
+                   int seq_q, int head_dim, float scale_log2, int causal, int dtype, void* stream,
+                   int n_split = 0, float* part_ws = nullptr, int* part_cnt = nullptr);
 
 }  // namespace
 
@@ -328,6 +330,19 @@ int gqa_paged_fwd_chunks_launch(const void* q, const int64_t q_stride[4], const 
   return paged_fwd_impl(q, q_stride, k_cache, k_cache_stride, v_cache, v_cache_stride, block_table, table_stride,
                         seq_lens, q_start, q_len, block_size, max_seq_len, o, o_stride, lse, workspace, kv_splits,
                         batch, num_heads, num_kv_heads, seq_q, head_dim, scale_log2, causal, dtype, stream);
+}
+
+int gqa_paged_fwd_split_launch(const void* q, const int64_t q_stride[4], const void* k_cache,
+                               const int64_t k_cache_stride[4], const void* v_cache,
+                               const int64_t v_cache_stride[4], const int* block_table, int table_stride,
+                               const int* seq_lens, const int* q_start, const int* q_len, int block_size,
+                               int max_seq_len, void* o, const int64_t o_stride[4], float* lse, float* workspace,
+                               int* counters, int n_split, int batch, int num_heads, int num_kv_heads, int seq_q,
+                               int head_dim, float scale_log2, int causal, int dtype, void* stream) {
+  return paged_fwd_impl(q, q_stride, k_cache, k_cache_stride, v_cache, v_cache_stride, block_table, table_stride,
+                        seq_lens, q_start, q_len, block_size, max_seq_len, o, o_stride, lse, nullptr, 0, batch,
+                        num_heads, num_kv_heads, seq_q, head_dim, scale_log2, causal, dtype, stream, n_split,
+                        workspace, counters);
 }
 
 int gqa_paged_cache_write_launch(const void* k, const int64_t k_stride[3], const void* v,
@@ -572,7 +587,8 @@ int paged_fwd_impl(const void* q, const int64_t q_stride[4], const void* k_cache
                    const int* block_table, int table_stride, const int* seq_lens, const int* q_start,
                    const int* q_len, int block_size, int max_seq_len, void* o, const int64_t o_stride[4],
                    float* lse, float* workspace, int kv_splits, int batch, int num_heads, int num_kv_heads,
-                   int seq_q, int head_dim, float scale_log2, int causal, int dtype, void* stream) {
+                   int seq_q, int head_dim, float scale_log2, int causal, int dtype, void* stream,
+                   int n_split, float* part_ws, int* part_cnt) {
   int rc = check_dims(batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, dtype);
   if (rc) return rc;
   const int G = num_heads / num_kv_heads;
@@ -582,10 +598,18 @@ int paged_fwd_impl(const void* q, const int64_t q_stride[4], const void* k_cache
   if (block_size < 512 / head_dim || block_size > GQA_MAX_BLOCK_SIZE || (block_size & (block_size - 1)) != 0)
     return GQA_E_BLOCK;
   if (table_stride < 0 || (int64_t)table_stride * block_size < (int64_t)max_seq_len) return GQA_E_BLOCK;
+  const int block_m = gqa::kFwdRows / G;
+  const int n_mblk = (seq_q + block_m - 1) / block_m;
+  if (n_split < 0 || n_split > n_mblk || (n_split > 0 && kv_splits > 0)) return GQA_E_SPLITS;
   if (batch == 0 || seq_q == 0) return GQA_OK;
   if (seq_lens == nullptr) return GQA_E_NULL;
   if ((reinterpret_cast<uintptr_t>(seq_lens) & 3u) != 0) return GQA_E_STRIDE;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return GQA_E_STRIDE;
+  if (n_split > 0) {
+    if (part_ws == nullptr || part_cnt == nullptr) return GQA_E_NULL;
+    if ((reinterpret_cast<uintptr_t>(part_ws) & 15u) != 0 || (reinterpret_cast<uintptr_t>(part_cnt) & 3u) != 0)
+      return GQA_E_STRIDE;
+  }
   if (kv_splits > 0 && workspace == nullptr) return GQA_E_NULL;
   if (kv_splits > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return GQA_E_STRIDE;
   if ((rc = check_varlen(q_start, q_len))) return rc;
@@ -602,9 +626,16 @@ int paged_fwd_impl(const void* q, const int64_t q_stride[4], const void* k_cache
   p.v = cache_ref(v_cache, v_cache_stride);
   p.o = ref(o, o_stride);
   p.dm = Dims{batch, num_heads, num_kv_heads, seq_q, max_seq_len, head_dim, G, scale_log2, causal ? 1 : 0};
-  p.block_m = gqa::kFwdRows / G;
-  p.n_mblk = (seq_q + p.block_m - 1) / p.block_m;
+  p.block_m = block_m;
+  p.n_mblk = n_mblk;
   p.lse = lse;
+  // Split query blocks (two key halves merged by whichever finishes last,
+  // as in gqa_fwd_split_launch; no scheduling counters: one workgroup per
+  // item).
+  p.n_split = n_split;
+  p.part_ws = part_ws;
+  p.part_cnt = part_cnt;
+  p.sched = nullptr;
   p.block_table = block_table;
   p.seq_lens = seq_lens;
   p.table_stride = table_stride;

@@ -78,7 +78,8 @@ py::object split_decode(const at::Tensor& q, const at::Tensor& k, const at::Tens
 //   route 0: gqa_paged_split_first_launch into ws, then the combine into out
 //            (gqa_split_reduce_varlen_launch with variable query lengths,
 //            else gqa_split_reduce_lse_launch or gqa_split_reduce_launch);
-//   route 1: gqa_paged_fwd_launch;
+//   route 1: gqa_paged_fwd_launch, or with `splits` > 0 split query blocks
+//            gqa_paged_fwd_split_launch (ws, zeroed counters);
 //   route 2: gqa_paged_fwd_chunks_launch (ws, `splits` key chunks).
 // q and out are (batch, heads, seq_q, head_dim), or token-major
 // (tokens, heads, head_dim) when q_start / q_len are given.
@@ -86,13 +87,16 @@ void paged_forward(int64_t route, const at::Tensor& q, const at::Tensor& k_cache
                    const at::Tensor& block_table, int64_t table_stride, const at::Tensor& seq_lens,
                    const std::optional<at::Tensor>& q_start, const std::optional<at::Tensor>& q_len,
                    int64_t max_seq_len, const at::Tensor& out, const std::optional<at::Tensor>& lse,
-                   const std::optional<at::Tensor>& ws, int64_t splits, int64_t batch, int64_t seq_q,
+                   const std::optional<at::Tensor>& ws, const std::optional<at::Tensor>& counters,
+                   int64_t splits, int64_t batch, int64_t seq_q,
                    double scale_log2, bool causal, int64_t dtype) {
   if (k_cache.dim() != 4 || v_cache.dim() != 4) throw std::invalid_argument("paged_forward: 4-d caches expected");
   const bool varlen = q_start.has_value() && q_len.has_value();
   if (varlen ? q.dim() != 3 || out.dim() != 3 : q.dim() != 4 || out.dim() != 4)
     throw std::invalid_argument("paged_forward: q / out rank does not match the query layout");
-  if (route != 1 && !ws.has_value()) throw std::invalid_argument("paged_forward: workspace expected");
+  if ((route != 1 || splits > 0) && !ws.has_value()) throw std::invalid_argument("paged_forward: workspace expected");
+  if (route == 1 && splits > 0 && !counters.has_value())
+    throw std::invalid_argument("paged_forward: counters expected");
   const int H = static_cast<int>(q.size(1)), D = static_cast<int>(q.size(-1));
   const int Hkv = static_cast<int>(k_cache.size(2)), bs = static_cast<int>(k_cache.size(1));
   int64_t qs[4], os[4], ks[4], vs[4];
@@ -116,6 +120,13 @@ void paged_forward(int64_t route, const at::Tensor& q, const at::Tensor& k_cache
   const int* table = block_table.data_ptr<int>();
   const int* lens = seq_lens.data_ptr<int>();
   int rc;
+  if (route == 1 && S > 0) {
+    rc = gqa_paged_fwd_split_launch(q.data_ptr(), qs, k_cache.data_ptr(), ks, v_cache.data_ptr(), vs, table, ts,
+                                    lens, qst, qln, bs, ms, out.data_ptr(), os, lse_p, ws_p,
+                                    counters->data_ptr<int>(), S, B, H, Hkv, Sq, D, sl2, causal ? 1 : 0, dt, stream);
+    if (rc != GQA_OK) raise_rc(rc, "gqa_paged_fwd_split_launch");
+    return;
+  }
   if (route == 1) {
     rc = gqa_paged_fwd_launch(q.data_ptr(), qs, k_cache.data_ptr(), ks, v_cache.data_ptr(), vs, table, ts, lens,
                               qst, qln, bs, ms, out.data_ptr(), os, lse_p, B, H, Hkv, Sq, D, sl2, causal ? 1 : 0,
@@ -173,7 +184,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("paged_forward", &paged_forward, "paged attention: one of the three kernel routes from tensors",
         py::arg("route"), py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"),
         py::arg("table_stride"), py::arg("seq_lens"), py::arg("q_start"), py::arg("q_len"), py::arg("max_seq_len"),
-        py::arg("out"), py::arg("lse"), py::arg("ws"), py::arg("splits"), py::arg("batch"), py::arg("seq_q"),
+        py::arg("out"), py::arg("lse"), py::arg("ws"), py::arg("counters"), py::arg("splits"), py::arg("batch"),
+        py::arg("seq_q"),
         py::arg("scale_log2"), py::arg("causal"), py::arg("dtype"));
   m.def("cache_write", &cache_write, "store new tokens' K/V at their paged cache slots", py::arg("key"),
         py::arg("value"), py::arg("k_cache"), py::arg("v_cache"), py::arg("slot_mapping"), py::arg("dtype"));

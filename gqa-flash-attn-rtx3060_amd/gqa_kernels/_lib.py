@@ -21,7 +21,7 @@ GQA_MAX_BLOCK_SIZE = 65536
 GQA_PAGED_CHUNK_PAGES = 2048
 GQA_NOALLOC_SCRATCH_BYTES = 16 << 20
 GQA_E_SCRATCH = -9
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _i64x4 = ctypes.c_int64 * 4
 _i64x3 = ctypes.c_int64 * 3
@@ -86,6 +86,11 @@ SIGNATURES = {
     "gqa_paged_fwd_chunks_launch": (
         _i,
         [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _p, _p, _i, _i, _p, _i64x4, _p, _p, _i,
+         _i, _i, _i, _i, _i, _f, _i, _i, _p],
+    ),
+    "gqa_paged_fwd_split_launch": (
+        _i,
+        [_p, _i64x4, _p, _i64x4, _p, _i64x4, _p, _i, _p, _p, _p, _i, _i, _p, _i64x4, _p, _p, _p, _i,
          _i, _i, _i, _i, _i, _f, _i, _i, _p],
     ),
     "gqa_paged_cache_write_launch": (

@@ -303,12 +303,13 @@ def choose_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
 
 
 def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, seq_kv: int,
-                     cu_count: int, causal: bool, head_dim: int = 128) -> int:
+                     cu_count: int, causal: bool, head_dim: int = 128, persistent: bool = None) -> int:
     """Query blocks per (b, kv head) to run as two key halves (0: none).
 
     Only causal blocks differ in length; when there are few workgroups per
     CU the longest block sets the run time, and splitting the heaviest ones
-    shortens it (fwd_split_makespan picks the count)."""
+    shortens it (fwd_split_makespan picks the count).  `persistent`
+    (default: head_dim 128) as fwd_split_makespan; False for paged caches."""
     group = num_heads // num_kv_heads
     block_m = max(1, FWD_ROWS // group)
     n_mblk = _cdiv(seq_q, block_m)
@@ -316,7 +317,8 @@ def choose_fwd_split(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, 
     if not causal or n_mblk < 2 or n_mblk * n_bh >= FWD_SPLIT_MAX_WG_PER_CU * cu_count:
         return 0
     tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, seq_kv, causal)
-    persistent = head_dim == 128
+    if persistent is None:
+        persistent = head_dim == 128
     base = fwd_split_makespan(tiles, 0, n_bh, cu_count, persistent=persistent)
     best, best_ns = base, 0
     for f in (0.25, 0.375, 0.5, 0.625, 0.75, 1.0):

@@ -40,8 +40,9 @@ from typing import Dict, Hashable, List, Optional, Sequence
 import torch
 
 from . import _lib
-from .dispatch import SPLIT_MIN_KV, choose_kv_chunks
-from .gqa_split import _decode_host, _workspace_buffer, stream_handle, workspace_bytes
+from .dispatch import (FWD_ROWS, SPLIT_MIN_KV, _fwd_block_tiles, choose_fwd_split, choose_kv_chunks,
+                       fwd_split_makespan)
+from .gqa_split import _counter_buffer, _decode_host, _workspace_buffer, stream_handle, workspace_bytes
 
 __all__ = [
     "paged_attention",
@@ -49,6 +50,7 @@ __all__ = [
     "paged_chunk",
     "paged_splits",
     "paged_kv_chunks",
+    "paged_single_plan",
     "PagedKVCache",
     "PagedAttentionMetadata",
     "GQAPagedAttention",
@@ -209,23 +211,43 @@ def paged_route(num_heads: int, num_kv_heads: int, seq_q: int, block_size: int, 
 
 
 @functools.lru_cache(maxsize=4096)
+def paged_single_plan(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
+                      cu_count: int, causal: bool = True, head_dim: int = 128):
+    """(key chunks, split blocks) for the paged single pass, at most one of
+    them non-zero.
+
+    The paged single pass runs one workgroup per query block.  Under causal
+    masking the last blocks of a sequence see the most keys and set the run
+    time when there are few workgroups per CU; running the heaviest ones as
+    two key halves (gqa_paged_fwd_split_launch) shortens that chain
+    (dispatch.choose_fwd_split).  With fewer blocks than compute units
+    against long sequences (a chunk of new tokens over a long cached prefix,
+    few sequences) most CUs idle, and splitting every block's key range
+    (gqa_paged_fwd_chunks_launch) fills them at the cost of the fp32
+    partials and the combine launch (dispatch.choose_kv_chunks, against the
+    split single pass, from SPLIT_MIN_KV keys on: the length from which the
+    reference splits the key axis at all).  The models are those of the
+    contiguous route for a kernel of one workgroup per item.  Cached: every
+    layer of a model step asks with the same arguments."""
+    n_split = choose_fwd_split(batch, num_heads, num_kv_heads, seq_q, max_seq_len, cu_count, causal, head_dim,
+                               persistent=False)
+    block_m = max(1, FWD_ROWS // (num_heads // num_kv_heads))
+    n_mblk = -(-seq_q // block_m)
+    if n_mblk * num_kv_heads * batch < cu_count and seq_q > 0 and max_seq_len >= SPLIT_MIN_KV:
+        tiles = _fwd_block_tiles(n_mblk, block_m, seq_q, max_seq_len, causal)
+        base = fwd_split_makespan(tiles, n_split, num_kv_heads * batch, cu_count, causal, persistent=False)
+        kc = choose_kv_chunks(batch, num_heads, num_kv_heads, seq_q, max_seq_len, cu_count, causal, head_dim, base,
+                              persistent=False)
+        if kc:
+            return kc, 0
+    return 0, n_split
+
+
 def paged_kv_chunks(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_seq_len: int,
                     cu_count: int, causal: bool = True, head_dim: int = 128) -> int:
-    """Key chunks per query block for the paged single pass (0: none).
-
-    The paged single pass runs one workgroup per query block; with fewer
-    blocks than compute units against long sequences (a chunk of new tokens
-    over a long cached prefix, few sequences) most CUs idle, and splitting
-    every block's key range (gqa_paged_fwd_chunks_launch) fills them, at the
-    cost of the fp32 partials and the combine launch: the count of
-    dispatch.choose_kv_chunks for a kernel of one workgroup per item, from
-    SPLIT_MIN_KV keys on (the length from which the reference splits the key
-    axis at all).  Cached: every layer of a model step asks with the same
-    arguments."""
-    if max_seq_len < SPLIT_MIN_KV:
-        return 0
-    return choose_kv_chunks(batch, num_heads, num_kv_heads, seq_q, max_seq_len, cu_count, causal, head_dim,
-                            persistent=False)
+    """Key chunks per query block for the paged single pass (0: none; see
+    paged_single_plan)."""
+    return paged_single_plan(batch, num_heads, num_kv_heads, seq_q, max_seq_len, cu_count, causal, head_dim)[0]
 
 
 def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
@@ -254,8 +276,10 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             max_blocks_per_seq * block_size, which needs no device read.
         scale: score scale (default head_dim ** -0.5, the reference's).
         splits: split count of the split route (default: ``paged_splits``),
-            or key chunks per query block of the "chunks" route (default:
-            ``paged_kv_chunks``, at least 2).
+            key chunks per query block of the "chunks" route (default:
+            ``paged_kv_chunks``, at least 2), or query blocks run as two key
+            halves on the "single" route (default: none when "single" is
+            forced, ``paged_single_plan``'s count when routed).
         return_lse: also return the natural-log LSE per row, fp32
             (batch, num_heads, seq_q).
         out: optional (batch, num_heads, seq_q, head_dim) tensor of q's dtype
@@ -331,27 +355,38 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
     lib = _lib.load()
     dtype = _DTYPES[q.dtype]
     stream = stream_handle(qdev)
-    kv_chunks = 0
+    kv_chunks = fwd_split = 0
     if route is None:
         route = paged_route(num_heads, num_kv_heads, seq_q, block_size, head_dim)
         if route == "single":
-            kv_chunks = paged_kv_chunks(batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev),
-                                        causal, head_dim)
+            kv_chunks, fwd_split = paged_single_plan(batch, num_heads, num_kv_heads, seq_q, max_seq_len,
+                                                     _cu_count(dev), bool(causal), head_dim)
             route = "chunks" if kv_chunks else route
+    elif route == "single":
+        fwd_split = splits if splits_given else 0
     elif route == "chunks":
         kv_chunks = splits if splits_given else max(2, paged_kv_chunks(
             batch, num_heads, num_kv_heads, seq_q, max_seq_len, _cu_count(dev), causal, head_dim))
     assert route in ("split", "single", "chunks")
     assert route == "split" or block_size >= single_pass_min_block(head_dim)
     lse = torch.empty(lse_shape, dtype=torch.float32, device=qdev) if return_lse else None
-    n_parts = kv_chunks if route == "chunks" else splits
-    workspace = None if route == "single" else _workspace_buffer(
-        qdev, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, n_parts))
+    counters = None
+    if route == "single":
+        # Split query blocks: their halves' fp32 state and the stream's
+        # zeroed merge counters (left zero by the kernel).
+        n_parts = fwd_split
+        workspace = None if not fwd_split else _workspace_buffer(
+            qdev, stream, lib.gqa_fwd_split_workspace_bytes(batch, num_kv_heads, head_dim, fwd_split))
+        if fwd_split:
+            counters = _counter_buffer(qdev, stream, lib.gqa_fwd_split_counters_count(batch, num_kv_heads, fwd_split))
+    else:
+        n_parts = kv_chunks if route == "chunks" else splits
+        workspace = _workspace_buffer(qdev, stream, workspace_bytes(batch, num_heads, seq_q, head_dim, n_parts))
     host = _paged_host()
     if host is not None:
         host.paged_forward(_ROUTE_IDS[route], q, k_cache, v_cache, block_table, table_stride, seq_lens,
                            query_start if varlen else None, query_lens if varlen else None, max_seq_len, out, lse,
-                           workspace, n_parts, batch, seq_q, scale * LOG2E, bool(causal), dtype)
+                           workspace, counters, n_parts, batch, seq_q, scale * LOG2E, bool(causal), dtype)
         return out if lse is None else (out, lse)
     # Token-major q / o as the kernels address them: (unused, head, token, d).
     qst = _lib._i64x4(0, q.stride(1), q.stride(0), 1) if varlen else _lib.strides(q)
@@ -366,6 +401,14 @@ def paged_attention(q, k_cache, v_cache, block_table, seq_lens, causal=True, *,
             seq_lens.data_ptr(), qs_p, ql_p, block_size, max_seq_len, out.data_ptr(), ost,
             lse_p, workspace.data_ptr(), kv_chunks, batch, num_heads, num_kv_heads, seq_q, head_dim,
             scale * LOG2E, int(bool(causal)), dtype, stream))
+        return out if lse is None else (out, lse)
+    if route == "single" and fwd_split:
+        _lib.check(lib.gqa_paged_fwd_split_launch(
+            q.data_ptr(), qst, k_cache.data_ptr(), _lib.strides(k_cache),
+            v_cache.data_ptr(), _lib.strides(v_cache), block_table.data_ptr(), table_stride,
+            seq_lens.data_ptr(), qs_p, ql_p, block_size, max_seq_len, out.data_ptr(), ost,
+            lse_p, workspace.data_ptr(), counters.data_ptr(), fwd_split, batch, num_heads, num_kv_heads, seq_q,
+            head_dim, scale * LOG2E, int(bool(causal)), dtype, stream))
         return out if lse is None else (out, lse)
     if route == "single":
         _lib.check(lib.gqa_paged_fwd_launch(
@@ -687,8 +730,8 @@ class GQAPagedAttention(torch.nn.Module):
             route, splits = kind, None
             if kind == "single":
                 dev = query.device.index if query.device.index is not None else torch.cuda.current_device()
-                kc = paged_kv_chunks(n, H, Hkv, max_q, max_seq_len, _cu_count(dev), self.causal, D)
-                route, splits = ("chunks", kc) if kc else ("single", None)
+                kc, ns = paged_single_plan(n, H, Hkv, max_q, max_seq_len, _cu_count(dev), bool(self.causal), D)
+                route, splits = ("chunks", kc) if kc else ("single", ns)
             paged_attention(q3, k_cache, v_cache, tables, lens, self.causal, max_seq_len=max_seq_len,
                             scale=self.scale, out=o3, route=route, splits=splits, query_start=qs,
                             query_lens=ql, max_query_len=max_q)

@@ -364,6 +364,30 @@ int gqa_paged_fwd_chunks_launch(const void* q, const int64_t q_stride[4],
                                 int seq_q, int head_dim,
                                 float scale_log2, int causal, int dtype, void* stream);
 
+/* gqa_paged_fwd_launch with the n_split heaviest query blocks of every
+ * (sequence, kv head) run as two work items over the two halves of their key
+ * range, merged by whichever finishes last — gqa_fwd_split_launch's split
+ * over a paged cache (no counterpart in the reference, whose single pass
+ * runs every query block as one program, gqa_kernels/dispatch.py:47-61).
+ * Arguments as gqa_paged_fwd_launch, plus workspace:
+ * gqa_fwd_split_workspace_bytes(batch, num_kv_heads, head_dim, n_split)
+ * bytes, 16-byte aligned; counters: at least batch * num_kv_heads * n_split
+ * int32 (gqa_fwd_split_counters_count serves), zero on the first call and
+ * left zero (one buffer serves every call on one stream; calls that overlap
+ * in time need separate buffers).  n_split in [0, ceil(seq_q / (256 / G))]
+ * (0: gqa_paged_fwd_launch), else GQA_E_SPLITS. */
+int gqa_paged_fwd_split_launch(const void* q, const int64_t q_stride[4],
+                               const void* k_cache, const int64_t k_cache_stride[4],
+                               const void* v_cache, const int64_t v_cache_stride[4],
+                               const int* block_table, int table_stride,
+                               const int* seq_lens, const int* q_start, const int* q_len,
+                               int block_size, int max_seq_len,
+                               void* o, const int64_t o_stride[4], float* lse,
+                               float* workspace, int* counters, int n_split,
+                               int batch, int num_heads, int num_kv_heads,
+                               int seq_q, int head_dim,
+                               float scale_log2, int causal, int dtype, void* stream);
+
 /* gqa_split_reduce_launch for variable query lengths (q_start, q_len as
  * above, non-NULL; o token-major); lse may be NULL or receives (tokens,
  * num_heads). */

@@ -209,6 +209,33 @@ def test_paged_chunks_empty_is_noop(lib):
     assert _pchunks(lib, B=0, q=None, k=None, v=None, table=None, lens=None, o=None, ws=None) == 0
 
 
+def _psplit(lib, ws=_FAKE, cnt=_FAKE, n_split=1, **kw):
+    a = dict(q=_FAKE, qs=_S4, k=_FAKE, ks=_C4, v=_FAKE, vs=_C4, table=_FAKE, tstride=16, lens=_FAKE,
+             qstart=None, qlen=None, bs=64, max_len=1024, o=_FAKE, os=_S4, lse=None, B=2, Hq=32, Hkv=8, Sq=128,
+             D=128, scale=0.1275, causal=1, dtype=0)
+    a.update(kw)
+    return lib.gqa_paged_fwd_split_launch(a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["table"],
+                                          a["tstride"], a["lens"], a["qstart"], a["qlen"], a["bs"], a["max_len"],
+                                          a["o"], a["os"], a["lse"], ws, cnt, n_split, a["B"], a["Hq"], a["Hkv"],
+                                          a["Sq"], a["D"], a["scale"], a["causal"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    # 128 queries at G = 4 are two 64-query blocks: n_split in [0, 2]
+    (dict(n_split=3), -5), (dict(n_split=-1), -5),
+    (dict(ws=None), -7), (dict(cnt=None), -7),                        # split state and counters: non-NULL
+    (dict(ws=ctypes.c_void_p((1 << 20) + 8)), -4),                    # workspace 16-byte aligned
+    (dict(cnt=ctypes.c_void_p((1 << 20) + 2)), -4),                   # counters 4-byte aligned
+    (dict(bs=2), -8), (dict(lens=None), -7), (dict(D=96), -2),        # as gqa_paged_fwd_launch
+])
+def test_paged_fwd_split_validation(lib, kw, code):
+    assert _psplit(lib, **kw) == code
+
+
+def test_paged_fwd_split_empty_is_noop(lib):
+    assert _psplit(lib, B=0, q=None, k=None, v=None, table=None, lens=None, o=None, ws=None, cnt=None) == 0
+
+
 def test_reduce_varlen_validation(lib):
     r = lib.gqa_split_reduce_varlen_launch
     assert r(_FAKE, 8, _FAKE, _S4, None, None, None, 2, 32, 16, 128, 0, None) == -7
