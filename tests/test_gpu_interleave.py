@@ -2,9 +2,9 @@
 behind changes another's result.
 
 Several paths keep state in device memory between calls: the persistent
-prefill's dynamic-schedule counters and the key-split blocks' merge counters
-(zero on entry, left zero by the last workgroup), the fused combine's
-counters, the stream's cached split workspace and counter buffers, and the
+prefill's dynamic-schedule counters and the key-split blocks' merge
+counters (contiguous and paged; zero on entry, left zero by the last
+workgroup), the fused combine's counters, the stream's cached split workspace and counter buffers, and the
 no-allocation entry point's fixed per-device buffer.  Each call kind below
 is first run alone (synchronised) for its reference result; then a seeded
 random sequence of 60 calls of all kinds runs back to back on the stream
@@ -123,6 +123,19 @@ def _kinds():
             _check(out[0], out[1], q, kc, vc, table, seq_lens, True, torch.bfloat16)
 
         kinds[name] = (pcall, pcheck)
+
+    # Paged single pass with split query blocks (merge counters in the same
+    # per-stream counter buffer as the prefill's).
+    q, kc, vc, table, seq_lens = _paged_inputs(2, 32, 8, 256, [3000, 1200], 128, 16, torch.bfloat16, seed=5)
+    sargs = (q.to(DEV), kc.to(DEV), vc.to(DEV), table.to(DEV), seq_lens.to(DEV), True)
+
+    def scall():
+        return paged_attention(*sargs, max_seq_len=3000, return_lse=True, route="single", splits=4)
+
+    def scheck(out, q=q, kc=kc, vc=vc, table=table, seq_lens=seq_lens):
+        _check(out[0], out[1], q, kc, vc, table, seq_lens, True, torch.bfloat16)
+
+    kinds["paged split blocks"] = (scall, scheck)
     return kinds
 
 
