@@ -6,8 +6,8 @@ TFLOP/s at the Llama-3.1-8B GQA shape, seq 16384 (B=1, Hq=32, Hkv=8, D=128,
 bf16); the ``decode`` object carries split-KV decode at seq_kv 131072
 (microseconds and HBM GB/s), ``paged_decode`` the same decode over a paged
 KV cache (gqa_kernels.paged) at two block sizes / in-block layouts,
-``paged_prefill`` the chunked-prefill shape over a paged cache (and a
-128-token chunk over a 16384-key paged prefix), and
+``paged_prefill`` the chunked-prefill shape over a paged cache (and
+chunks over 16384-key paged prefixes), and
 ``configs`` every BASELINE config (prefill 2048-16384, decode 2048-131072,
 chunked prefill, the 70B decode shape) with its time and the fraction of the
 roofline (MFMA or HBM) that bounds it, ``extras`` the same for a 16-token
@@ -478,12 +478,14 @@ def paged_prefill(torch, steps, warmup):
     """The chunked-prefill BASELINE shape (B=4, 512 new tokens attending 8192
     keys, causal) over a paged cache (gqa_kernels.paged, single-pass route),
     128-key HND blocks, 64-key NHD blocks and 16-key NHD blocks (vLLM's
-    default block size) in random order; then one sequence's 128-token
-    chunk over a 16384-key prefix in 16-key NHD blocks (the key-chunk
-    route)."""
+    default block size) in random order; then two sequences' 512-token
+    chunks over 16384 keys (the single pass with split query blocks) and
+    one sequence's 128-token chunk over a 16384-key prefix (the key-chunk
+    route), in 16-key NHD blocks."""
     from gqa_kernels.paged import paged_attention
     out = []
     for b, sq, skv, legs in ((4, 512, 8192, ((128, "HND"), (64, "NHD"), (16, "NHD"))),
+                             (2, 512, 16384, ((16, "NHD"),)),
                              (1, 128, 16384, ((16, "NHD"),))):
         out += _paged_prefill_legs(torch, paged_attention, b, sq, skv, legs, steps, warmup)
     return out
