@@ -140,8 +140,9 @@ def test_sweep(case):
 # Paged KV cache (gqa_kernels.paged.paged_attention) against the oracle's
 # paged_reference: random page sizes 1-256, token-major (NHD) and head-major
 # (HND) pages, ragged per-sequence lengths (a sequence may hold no key),
-# decode to chunked query blocks; the default route and, where the page size
-# allows it, the other one.
+# decode to chunked query blocks; the split-KV route and, where the page size
+# allows it, the single pass (plain and with every query block split), then
+# the default route (key chunks or split blocks where the plan takes them).
 # --------------------------------------------------------------------------
 N_PAGED = 40
 
@@ -191,10 +192,17 @@ def test_paged_sweep(case):
     if hnd:
         kd, vd = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (kc, vc))
     args = (q.to(DEV), kd, vd, table.to(DEV), seq_lens.to(DEV), causal)
-    routes = ["split"] + (["single"] if bs >= single_pass_min_block(D) else [])
+    # Both kernel routes, the single pass with every query block split in
+    # two key halves, and the default route (which may take key chunks or
+    # split blocks by paged_single_plan).
+    legs = [("split", None)]
+    if bs >= single_pass_min_block(D):
+        n_mblk = -(-Sq // max(1, 256 // (Hq // Hkv)))
+        legs += [("single", None), ("single", n_mblk)]
+    legs.append((None, None))
     default = paged_route(Hq, Hkv, Sq, bs, D)
-    for route in routes:
-        print(f"paged sweep {_paged_id(case)} route={route} (default {default})", flush=True)
-        o, lse = paged_attention(*args, max_seq_len=max(lens), return_lse=True, route=route)
+    for route, splits in legs:
+        print(f"paged sweep {_paged_id(case)} route={route} splits={splits} (default {default})", flush=True)
+        o, lse = paged_attention(*args, max_seq_len=max(lens), return_lse=True, route=route, splits=splits)
         torch.cuda.synchronize()
         _check(o, lse, q, kc, vc, table, seq_lens, causal, dtype)
