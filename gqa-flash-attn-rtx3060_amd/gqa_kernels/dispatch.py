@@ -43,7 +43,10 @@ SPLIT_MAX_ROWS = 64
 # keys 16.0 / 16.7, 32768 keys 25.6 / 27.3, 65536 keys 44.0-44.3 / 45.1-45.3,
 # 131072 keys 83.5-84.8 / 82.4-82.8 (so 64 only there); 16 tokens at 32768
 # keys 35.7 / 41.5; 32 tokens at 32768 keys (128-row workgroups) 256
-# workgroups 41 us, 512 51 us.
+# workgroups 41 us, 512 51 us.  64-row workgroups (33-64 packed rows) need
+# chunks of twice this: 16 tokens at 131072 keys 32 splits 92.2 us / 64
+# 96.2 (8 tokens, 32-row workgroups: 87.7 / 88.7; 32 tokens, 128-row
+# workgroups: 112.0 / 107.2).
 SPLIT_WIDER_MIN_CHUNK = 2048
 # Shortest key cache worth splitting (the reference's threshold, dispatch.py:37).
 SPLIT_MIN_KV = 1024
@@ -347,13 +350,14 @@ def split_count(base: int, seq_kv: int, cu_count: int, rows_per_wg: int, head_di
     """Split count of the split-KV path for `base` workgroups per split
     (head_dim 128, and head_dim 64 when the 16-row first pass runs
     (`rows16`: at most DEC16_ROWS packed rows): fill the CUs, then a second
-    workgroup per CU only for chunks of SPLIT_WIDER_MIN_CHUNK keys; head_dim
+    workgroup per CU only for chunks of SPLIT_WIDER_MIN_CHUNK keys (twice
+    that for 64-row workgroups); head_dim
     64 over more rows: two workgroups per CU with chunks of SPLIT_MIN_TILES
     tiles)."""
     target = SPLIT_WG_PER_CU * cu_count
     splits = 1
     if head_dim == 128 or rows_per_wg > SPLIT_WIDE_ROWS or rows16:
-        wider_min = SPLIT_WIDER_MIN_CHUNK * (2 if head_dim == 64 else 1)
+        wider_min = SPLIT_WIDER_MIN_CHUNK * (2 if head_dim == 64 or rows_per_wg == SPLIT_WIDE_ROWS else 1)
         while (base * splits < cu_count and splits < _lib.GQA_MAX_SPLITS
                and _cdiv(seq_kv, splits * 2) >= SPLIT_MIN_TILES * SPLIT_TILE):
             splits *= 2

@@ -63,13 +63,15 @@ def test_abi_version_and_strerror(lib):
 
 
 def test_host_binding_loads(lib):
-    """The torch-tensor binding of the decode call (_gqa_host.so) loads,
-    links against the same library ABI and exposes split_decode (no GPU
-    work: the binding is exercised by the GPU decode tests)."""
+    """The torch-tensor binding of the decode and paged calls (_gqa_host.so)
+    loads, links against the same library ABI and exposes split_decode,
+    paged_forward and cache_write (no GPU work: the binding is exercised by
+    the GPU decode and paged tests)."""
     from gqa_kernels import _lib
     host = _lib.load_host()
     assert host.ABI_VERSION == lib.gqa_abi_version() == _lib.ABI_VERSION
     assert callable(host.split_decode)
+    assert callable(host.paged_forward) and callable(host.cache_write)
     assert _lib.load_host() is host
 
 
@@ -271,8 +273,11 @@ def test_route_wide_row_blocks():
     assert split_rows_per_workgroup(32) == 32 and split_rows_per_workgroup(33) == 64
     assert split_rows_per_workgroup(64, 64) == 32
     for sq in (9, 16):
+        # 64-row workgroups: the second doubling needs 4096-key chunks
+        # (16 tokens at 131072 keys: 32 splits 92.2 us, 64 splits 96.2)
         r = choose_route(1, 32, 8, sq, 131072, cu)
-        assert r.kind == "split" and r.splits == 64 and r.workgroups == 512
+        assert r.kind == "split" and r.splits == 32 and r.workgroups == 256
+        assert choose_route(1, 32, 8, sq, 262144, cu).splits == 64
         # 32768 keys: the CUs filled once
         assert choose_route(1, 32, 8, sq, 32768, cu).splits == 32
         r64 = choose_route(1, 32, 8, sq, 131072, cu, True, 64)
