@@ -79,6 +79,22 @@ _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 # 8192 44.7 / 46.1 / 47.2; token-major 16-key pages 131072 keys 51.0 / 52.3
 # / 52.8, B = 4 x 32768 53.5 / 48.6 / 48.9, B = 16 x 8192 54.0 / 56.2 /
 # 49.5.
+# Batches of several sequences: the counts above assume every sequence is
+# max_seq_len keys long; with unequal lengths the longest sequences' few
+# long chunks set the run time, so such a batch is cut into at least
+# _BATCH_MIN_SPLITS chunks per sequence while chunks keep _MIN_CHUNK keys
+# and the first pass stays within _BATCH_MAX_WG_PER_CU workgroups per CU.
+# Measured (16-key pages, one token, us, the count chosen before -> after):
+# lengths random in 100-8000, B = 32: token-major 4 -> 8 splits 113.3 ->
+# 107.3, head-major 1 -> 8 120.2 -> 108.2; 500-16000, B = 16: head-major
+# 2 -> 8 121.0 -> 109.6 (token-major already 8); 1000-30000, B = 8:
+# head-major 4 -> 8 113.4 -> 101.2; 100-4000, B = 64: token-major 2 -> 4
+# 122.8 -> 120.0, head-major 1 -> 4 113.5 -> 116.7 (8 splits: 119.9, so the
+# workgroup cap); eight such batches 929 -> 887 us in all.  Uniform lengths
+# pay: B = 32 x 4096 head-major 82.8 -> 88.5, B = 8 x 16384 82.9 -> 84.9
+# (four uniform batches 345 -> 353 us).
+_BATCH_MIN_SPLITS = 8
+_BATCH_MAX_WG_PER_CU = 8
 _SPLIT_ROWS = 32
 _SPLIT_WG_PER_CU = 2
 _LDS_WG_PER_CU = 1
@@ -120,7 +136,9 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
     packed rows and pages of >= 8 keys — one, or four for a single-token
     step of a batch over pages whose heads are interleaved; else two) while every chunk keeps at
     least 256 keys (pure function of the shapes and of ``heads_interleaved``:
-    the cache's slot stride differs from head_dim).  With pages under 64 keys a chunk spans
+    the cache's slot stride differs from head_dim); a batch of several
+    sequences, whose lengths may differ, gets at least 8 chunks per sequence
+    within 8 workgroups per CU.  With pages under 64 keys a chunk spans
     at most GQA_PAGED_CHUNK_PAGES pages (the slice of the block table a
     workgroup stages in LDS), which can ask for more splits."""
     group = num_heads // num_kv_heads
@@ -143,6 +161,10 @@ def paged_splits(batch: int, num_heads: int, num_kv_heads: int, seq_q: int, max_
     while (base * splits < target and splits < _lib.GQA_MAX_SPLITS
            and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
         splits *= 2
+    if batch > 1:
+        while (splits < _BATCH_MIN_SPLITS and base * splits * 2 <= _BATCH_MAX_WG_PER_CU * cu_count
+               and -(-max_seq_len // (splits * 2)) >= _MIN_CHUNK):
+            splits *= 2
     if block_size < 64:
         def too_many_pages(s):
             return paged_chunk(max_seq_len, s) // block_size > _lib.GQA_PAGED_CHUNK_PAGES

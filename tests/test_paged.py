@@ -287,7 +287,12 @@ def test_paged_splits():
     assert paged_splits(1, 32, 8, 8, 131072, 256, head_dim=64) == 64
     assert paged_splits(1, 32, 8, 1, 131072, 256, block_size=4, head_dim=64) == 64
     assert paged_splits(1, 32, 8, 1, 131072, 256, block_size=2) == 64
-    assert paged_splits(64, 32, 8, 1, 4096, 256) == 1
+    # a batch of several sequences (lengths may differ): at least 8 chunks
+    # per sequence within 8 workgroups per CU
+    assert paged_splits(64, 32, 8, 1, 4096, 256) == 4
+    assert paged_splits(8, 32, 8, 1, 30000, 256) == 8
+    assert paged_splits(32, 32, 8, 1, 8000, 256) == 8
+    assert paged_splits(32, 32, 8, 1, 1000, 256) == 2  # chunks keep 256 keys
     assert paged_splits(1, 32, 8, 1, 300, 256) == 1
     for L in (256, 1000, 5000, 1 << 20):
         for B in (1, 3, 16):
@@ -300,11 +305,11 @@ def test_paged_splits_small_pages():
     from gqa_kernels import _lib
     from gqa_kernels.paged import paged_chunk, paged_splits
     assert paged_chunk(4096, 2) == 2048 and paged_chunk(300, 1) == 320 and paged_chunk(40000, 2) == 20032
-    # 512 workgroups from the batch alone: one split, unless a chunk would
-    # span more than 2048 pages
-    assert paged_splits(512, 8, 1, 1, 4096, 256) == 1
-    assert paged_splits(512, 8, 1, 1, 4096, 256, block_size=64) == 1
-    assert paged_splits(512, 8, 1, 1, 4096, 256, block_size=1) == 2
+    # 512 workgroups from the batch alone: 4 splits (8 workgroups per CU),
+    # more when a chunk would span more than 2048 pages
+    assert paged_splits(512, 8, 1, 1, 4096, 256) == 4
+    assert paged_splits(512, 8, 1, 1, 4096, 256, block_size=64) == 4
+    assert paged_splits(512, 8, 1, 1, 40000, 256, block_size=1) == 32
     assert paged_splits(512, 8, 1, 1, 1 << 20, 256, block_size=16) == 32
     for bs in (1, 2, 4, 8, 16, 32):
         for L in (1, 300, 2048, 2049, 70000, 1 << 20):
