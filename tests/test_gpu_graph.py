@@ -1,7 +1,8 @@
 """The public path under HIP graph capture (torch.cuda.CUDAGraph): decode
 steps (split-KV, two launches), the fused combine, prefill with and without
-the key split, and paged decode are captured once and replayed several
-times, with eager work and synchronisations between replays; every replay
+the key split, paged decode, the paged single pass with split blocks and
+over key chunks, and the vLLM-shaped layer's decode step with its K/V write
+are captured once and replayed several times, with eager work and synchronisations between replays; every replay
 must equal the eager result bit for bit (the kernels are deterministic and
 the captured launches see the same inputs)."""
 from __future__ import annotations
@@ -168,3 +169,49 @@ def test_two_graphs_replayed_concurrently(shape):
         torch.cuda.synchronize()
         for i, ((_, out), e) in enumerate(zip(graphs, expect)):
             assert torch.equal(out, e), f"replay {rep} of graph {i} differs from the eager result"
+
+
+def _paged_cache(lens, bs, seed):
+    from gqa_kernels.paged import PagedKVCache
+    g0 = torch.Generator().manual_seed(seed)
+    cache = PagedKVCache(sum(-(-n // bs) for n in lens) + 8, bs, 8, 128, dtype=torch.bfloat16, device=DEV,
+                         layout="NHD")
+    for s, n in enumerate(lens):
+        cache.add_sequence(s)
+        cache.append([s], torch.randn(n, 8, 128, generator=g0).to(torch.bfloat16).to(DEV),
+                     torch.randn(n, 8, 128, generator=g0).to(torch.bfloat16).to(DEV))
+    return cache, g0
+
+
+@pytest.mark.parametrize("case", ["split_blocks", "chunks", "layer_decode_write"])
+def test_paged_routes_in_graph(case):
+    """The paged single pass with split blocks (merge counters from the
+    capture's own zeroed buffer), the paged key chunks (workspace and the
+    combine) and the vLLM-shaped layer's decode step with its K/V write,
+    captured and replayed."""
+    from gqa_kernels.paged import GQAPagedAttention, PagedAttentionMetadata, paged_attention
+    print(f"paged graph {case}", flush=True)
+    if case == "layer_decode_write":
+        lens = [3000, 700, 1500]
+        cache, g0 = _paged_cache(lens, 16, 7)
+        slots = torch.tensor(sum((cache.reserve(s, 1) for s in range(3)), []), dtype=torch.int64, device=DEV)
+        md = PagedAttentionMetadata(slot_mapping=slots, block_tables=cache.block_table(range(3)),
+                                    seq_lens=cache.seq_lens(range(3)), query_len=1, max_seq_len=3001)
+        layer = GQAPagedAttention(32, 128, num_kv_heads=8)
+        query = torch.randn(3, 32 * 128, generator=g0).to(torch.bfloat16).to(DEV)
+        key = torch.randn(3, 8 * 128, generator=g0).to(torch.bfloat16).to(DEV)
+        value = torch.randn(3, 8 * 128, generator=g0).to(torch.bfloat16).to(DEV)
+        fn = lambda: layer(query, key, value, cache.kv, md)  # the same slots each time: idempotent
+    else:
+        lens = [3000, 1200] if case == "split_blocks" else [9000]
+        cache, g0 = _paged_cache(lens, 16, 11)
+        sq = 256 if case == "split_blocks" else 128
+        q = torch.randn(len(lens), 32, sq, 128, generator=g0).to(torch.bfloat16).to(DEV)
+        table, seq_lens = cache.block_table(range(len(lens))), cache.seq_lens(range(len(lens)))
+        route, splits = ("single", 4) if case == "split_blocks" else ("chunks", 8)
+        fn = lambda: paged_attention(q, cache.k_cache, cache.v_cache, table, seq_lens, True, max_seq_len=max(lens),
+                                     return_lse=True, route=route, splits=splits)
+    first = fn()
+    expect = tuple(t.clone() for t in first) if isinstance(first, tuple) else first.clone()
+    g, out = _capture(fn)
+    _replays(g, out, expect)
