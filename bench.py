@@ -415,6 +415,13 @@ def main() -> int:
             result["decode"]["cpu_baseline"] = cpu_decode_baseline(torch)
         del q, kvs
         torch.cuda.empty_cache()
+        # Context for `peak`: what a plain device copy (torch's copy kernel,
+        # reads and writes) moves per second on this box.
+        copy = copy_calibration(torch, 10, 3)
+        result["decode"]["roofline"]["copy_ceiling"] = {"kernel": "torch copy_ of 1 GiB fp32 (read + write)",
+                                                        "us": copy["ms"] * 1e3, "gbs": copy["gbs"]}
+        result["decode"]["roofline"]["frac_of_copy_ceiling"] = gbs / copy["gbs"]
+        torch.cuda.empty_cache()
 
     # ---------------- decode and chunked prefill over a paged KV cache ----------------
     if args.only in (None, "paged"):
