@@ -431,7 +431,12 @@ __global__ __launch_bounds__(256) void gqa_split_reduce_kernel(ReduceParams p) {
   __shared__ f32x4 red_o[NSG][ND4];
 
   const int t = threadIdx.x;
-  const int row = blockIdx.x;  // ((b * Hq + h) * Sq + pos)
+  // Row ((b * Hq + h) * Sq + pos), dealt to the XCDs in contiguous ranges:
+  // rows are ordered by (b, kv head) as the first passes' work items are,
+  // so a row is combined on the XCD whose L2 holds its partials (decode
+  // 8192 keys 10.89 -> 10.72 us, a 16-token verify step at 131072 keys
+  // 92.25 -> 91.28 us, bit-identical).
+  const int row = xcd_remap(blockIdx.x, gridDim.x);
   const int S = p.splits;
   const int pos = row % p.Sq;
   const int bh = row / p.Sq;
